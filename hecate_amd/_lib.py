@@ -1,0 +1,81 @@
+"""ctypes binding of libhecate_moe.so (include/hecate_moe.h). The product path has no fallback: if the library is
+missing or a call fails, a RuntimeError names it."""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libhecate_moe.so")
+_L = None
+
+P, i32, i64, u64, f32, sz = (ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float,
+                             ctypes.c_size_t)
+
+SIGNATURES = {
+    "hmoe_last_error": (ctypes.c_char_p, []),
+    "hmoe_version": (i32, []),
+    "hmoe_pack_i4": (i32, [P, P, i32, i32, P, P]),
+    "hmoe_unpack_i4": (i32, [P, P, i32, i32, P, P]),
+    "hmoe_pack_dense": (i32, [P, i32, i32, P]),
+    "hmoe_repack_moe4": (i32, [P, P, i32, i32, P, P]),
+    "hmoe_gen_i4": (i32, [u64, u64, f32, i32, i32, P, P, P]),
+    "hmoe_gen_dense": (i32, [u64, f32, i32, i32, P, P]),
+    "hmoe_gen_normal": (i32, [u64, i64, f32, f32, i32, P, P]),
+    "hmoe_router_scratch_bytes": (sz, [i32, i32]),
+    "hmoe_router_fused": (i32, [P, P, P, P, P, P, P, i32, i32, i32, i32, f32, P, P]),
+    "hmoe_moe4_scratch_bytes": (sz, [i32]),
+    "hmoe_moe4_forward": (i32, [P, P, P, i32, i32, P, P, P, P, P, P, P, P, P, P, P, P, i32, i32, i32,
+                                P, P, P, P, P, P, i32, P]),
+    "hmoe_moe4_gate_up": (i32, [P, P, P, i32, i32, P, P, P, P, P, P, P, i32, i32, P, P, i32, P]),
+    "hmoe_moe4_down": (i32, [P, P, i32, i32, P, P, P, P, P, P, i32, i32, P, P]),
+    "hmoe_moe4_combine": (i32, [P, P, P, i32, P, P, P]),
+    "hmoe_moe4_dequant": (i32, [P, P, i32, i32, P, P]),
+    "hmoe_finish_bf16": (i32, [P, i32, P, P]),
+    "hmoe_dispatch_work_bytes": (sz, [i32, i32, i32]),
+    "hmoe_dispatch_nrb_max": (i32, [i32, i32, i32]),
+    "hmoe_dispatch": (i32, [P, P, i32, i32, i32, i32, i32, i32, P, P, P, P, P, P, i32, P, P, P]),
+    "hmoe_moe4p_scratch_bytes": (sz, [i32, i32, i32]),
+    "hmoe_moe4p_forward": (i32, [P, P, P, P, P, i32, i32, i32, P, P, P, P, P, P, P, P, P, P, i32, P, P, i32, i32,
+                                 P, P, P, P]),
+    "hmoe_residual_rmsnorm": (i32, [P, P, P, i32, f32, P, P, P]),
+}
+
+
+def lib():
+    """the loaded library (raises if it has not been built: python -m hecate_amd.build_lib)"""
+    global _L
+    if _L is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"hecate_amd: {LIB_PATH} is missing; build it with python -m hecate_amd.build_lib")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _L = L
+    return _L
+
+
+def check(rc, what=""):
+    if rc != 0:
+        msg = lib().hmoe_last_error().decode(errors="replace")
+        raise RuntimeError(f"hecate_amd {what}: {msg} (status {rc})")
+
+
+def call(name, *args):
+    check(getattr(lib(), name)(*args), name)
+
+
+def ptr(t):
+    """device (or host) address of a torch tensor / numpy array / int, None for 0"""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t or None
+    if hasattr(t, "data_ptr"):
+        return t.data_ptr()
+    return t.ctypes.data
+
+
+def stream_of(device=None):
+    import torch
+    return torch.cuda.current_stream(device).cuda_stream

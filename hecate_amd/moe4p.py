@@ -1,0 +1,38 @@
+"""Prefill MoE operator: the drop-in for the reference's `moe4p` extension (runtime/tier/moe4/moe4p.cu:209-251).
+
+forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out) keeps the reference's names and order; the
+trailing keywords (inv, meta, topk, shared) are this build's additions: a deterministic per-token combine, sizes read
+from a device-side dispatch plan (no host sync), and the shared expert in the same call.
+"""
+import torch
+
+from ._lib import call, lib, ptr, stream_of
+
+H, I = 6144, 2048
+
+
+def scratch(dev, npos, T=0):
+    """moe4p.cu:209-215: [gu, ar, d] for up to npos picks (+ T rows for the shared expert)"""
+    dev = torch.device(dev)
+    L = lib()
+    return [torch.zeros(int(L.hmoe_moe4p_scratch_bytes(0, npos, T)) // 4, dtype=torch.float32, device=dev),
+            torch.empty((npos + T, I), dtype=torch.float16, device=dev),
+            torch.empty((npos + T, H), dtype=torch.float32, device=dev)]
+
+
+def forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, inv=None, meta=None, topk=8, shared=None,
+            npos=None, nrb=None):
+    """moe4p.cu:220-245: out[tok] += routed experts of the sorted picks (+ the shared expert on every token)"""
+    T = x.shape[0]
+    if not (x.dim() == 2 and x.shape[1] == H and x.dtype == torch.bfloat16 and out.dtype == torch.float32
+            and rbt.dim() == 2 and rbt.shape[1] == 4 and x.is_contiguous() and out.is_contiguous()):
+        raise RuntimeError("moe4p: shapes")
+    npos = tok.numel() if npos is None else npos
+    nrb = rbt.shape[0] if nrb is None else nrb
+    ps = ar.shape[0] - (T if shared is not None else 0)
+    if npos > ps or d.shape[0] < ar.shape[0]:
+        raise RuntimeError(f"moe4p: scratch holds {ps} picks, {npos} given")
+    sh = shared if shared is not None else (None, None, None)
+    call("hmoe_moe4p_forward", ptr(x), ptr(tok), ptr(eid), ptr(wt), ptr(rbt), int(npos), int(nrb), gw.numel(),
+         ptr(gw), ptr(uw), ptr(dw), ptr(gs), ptr(us), ptr(ds), ptr(gu), ptr(ar), ptr(d), ptr(out), int(ps),
+         ptr(meta), ptr(inv), int(T), int(topk), ptr(sh[0]), ptr(sh[1]), ptr(sh[2]), stream_of(x.device))

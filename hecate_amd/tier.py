@@ -1,0 +1,184 @@
+"""The GPU tier's MoE layer on one MI355X: what runtime/tier/tier_split.py does around the moe4 / moe4p ops
+(tier_split_load:171-269 resident expert tables, tier_submit:520-574 decode vs prefill, tier_combine:577-644) and the
+row-block planner of runtime/tier/rtx_split.py:236-255 (pick_groups), restated for this build's formats.
+
+Decode (<= 16 rows): router_fused (writes the f16 copy of x) -> moe4.forward(xf=1) (routed + shared expert into the
+fp32 accumulator) -> bf16 output (accumulator zeroed). Prefill: router -> device dispatch plan (no host sync) ->
+moe4p.forward (routed + shared) -> bf16 output. Every launch is static-shaped and allocation-free, so a whole step can
+be captured in a hipGraph.
+"""
+import numpy as np
+import torch
+
+from . import moe4, moe4p, router
+from ._lib import call, lib, ptr, stream_of
+
+H, I, TOPK = 6144, 2048, 8
+I4_Q_GU, I4_S_GU = I * H // 2, I * (H // 128) * 2          # bytes of one gate / up matrix (codes, scales)
+I4_Q_D, I4_S_D = H * I // 2, H * (I // 128) * 2            # bytes of one down matrix
+
+
+def pick_groups(counts, npos, bm=64, balance=False):
+    """rtx_split.py:236-255: picks sorted by expert, counts per expert; yields groups of whole experts holding at most
+    npos picks as (first pick, end pick, row blocks int32 [n, 4] {expert, first pick relative to the group, picks
+    <= bm, 0}). balance: an expert's blocks get near-equal sizes (base = c // nb, the first c % nb get one more)."""
+    c = np.asarray(counts, dtype=np.int64).reshape(-1)
+    n = c.size
+    end = np.cumsum(c)
+    start = end - c
+    e0 = 0
+    while e0 < n:
+        p0 = int(start[e0])
+        e1 = int(np.searchsorted(end, p0 + npos, side="right"))
+        if e1 <= e0:
+            raise ValueError(f"pick_groups: expert {e0} has {int(c[e0])} picks, more than npos {npos}")
+        rows_l = []
+        for e in range(e0, e1):
+            ce = int(c[e])
+            nb = (ce + bm - 1) // bm
+            for k in range(nb):
+                if balance:
+                    base, extra = divmod(ce, nb)
+                    rows, first = base + (1 if k < extra else 0), k * base + min(k, extra)
+                else:
+                    rows, first = min(bm, ce - bm * k), bm * k
+                rows_l.append((e, int(start[e]) - p0 + first, rows, 0))
+        rbt = np.array(rows_l, dtype=np.int32).reshape(-1, 4)
+        yield p0, int(end[e1 - 1]), rbt
+        e0 = e1
+
+
+class ExpertBank:
+    """int4 experts resident in HBM in the I4G128 layout: one buffer per matrix kind and int64 device tables of each
+    expert's addresses (the tables tier_split.py:206-214,246 builds), local ids 0..n-1"""
+
+    def __init__(self, n, device):
+        self.n = n
+        self.device = torch.device(device)
+        mk = lambda nb: torch.empty(max(n, 1) * nb, dtype=torch.uint8, device=self.device)
+        self.buf = {"gate_q": mk(I4_Q_GU), "gate_s": mk(I4_S_GU), "up_q": mk(I4_Q_GU), "up_s": mk(I4_S_GU),
+                    "down_q": mk(I4_Q_D), "down_s": mk(I4_S_D)}
+        self.size = {"gate_q": I4_Q_GU, "gate_s": I4_S_GU, "up_q": I4_Q_GU, "up_s": I4_S_GU, "down_q": I4_Q_D,
+                     "down_s": I4_S_D}
+        self.tab = {k: torch.tensor([self.addr(k, e) for e in range(max(n, 1))], dtype=torch.int64, device=self.device)
+                    for k in self.buf}
+
+    def addr(self, kind, e):
+        return self.buf[kind].data_ptr() + e * self.size[kind]
+
+    def view(self, kind, e):
+        return self.buf[kind][e * self.size[kind]:(e + 1) * self.size[kind]]
+
+    def tables(self):
+        t = self.tab
+        return t["gate_q"], t["up_q"], t["down_q"], t["gate_s"], t["up_s"], t["down_s"]
+
+    @property
+    def nbytes(self):
+        return sum(b.numel() for b in self.buf.values())
+
+
+class PrefillBuffers:
+    """device buffers of a prefill chunk of up to T rows: selection, dispatch plan (hmoe_dispatch), GEMM scratch"""
+
+    def __init__(self, T, topk, lo, n, E, device, bm=64):
+        dev = torch.device(device)
+        L = lib()
+        self.T, self.topk, self.lo, self.n, self.bm = T, topk, lo, n, bm
+        self.F = F = T * topk
+        self.nrb_max = int(L.hmoe_dispatch_nrb_max(F, n, bm))
+        z = lambda *shape, dt=torch.int32: torch.zeros(shape, dtype=dt, device=dev)
+        self.counts, self.tok, self.eid, self.inv = z(n), z(F), z(F), z(F)
+        self.wt = z(F, dt=torch.float32)
+        self.rbt, self.meta = z(self.nrb_max, 4), z(4)
+        self.work = z(int(L.hmoe_dispatch_work_bytes(T, topk, n)) // 4 + 1)
+        self.scr = moe4p.scratch(dev, F, T)
+        self.y = z(T, H, dt=torch.float32)
+        self.out = z(T, H, dt=torch.bfloat16)
+        self.sel, self.rw = z(T, topk, dt=torch.int64), z(T, topk, dt=torch.float16)
+        self.logits = z(int(L.hmoe_router_scratch_bytes(T, E)) // 4, dt=torch.float32)
+
+    def run(self, sel, rw, balance=False):
+        """device dispatch plan of a selection (tier_split.py:404-417 + pick_groups in one group), no host sync:
+        counts, tok / eid / wt sorted by (expert, flat index), inv, rbt rows, meta = {npos, nrb, nrb wanted, 0}"""
+        T = sel.shape[0]
+        if T > self.T:
+            raise RuntimeError(f"dispatch: {T} rows > {self.T}")
+        call("hmoe_dispatch", ptr(sel), ptr(rw), T, self.topk, self.lo, self.n, self.bm, int(bool(balance)),
+             ptr(self.counts), ptr(self.tok), ptr(self.eid), ptr(self.wt), ptr(self.inv), ptr(self.rbt),
+             self.nrb_max, ptr(self.meta), ptr(self.work), stream_of(sel.device))
+        return self
+
+
+class MoELayer:
+    """one routed int4 MoE layer: router (fp32 W_g [E, H], selection bias), resident experts for ids [lo, lo + n_hot)
+    (ExpertBank, local id = id - lo), optional F16T shared expert; max_rows bounds the prefill chunk"""
+
+    def __init__(self, wg, bias, bank, shared=None, lo=0, n_hot=None, topk=TOPK, scale=2.5, max_rows=16):
+        self.wg, self.bias, self.bank, self.shared = wg, bias, bank, shared
+        self.device = wg.device
+        self.E = wg.shape[0]
+        self.lo, self.n_hot = lo, bank.n if n_hot is None else n_hot
+        self.topk, self.scale = topk, scale
+        self.max_rows = max(max_rows, 16)
+        dev = self.device
+        self.logits, self.ctr = router.buffers(self.max_rows, dev, self.E)
+        self.sel = torch.zeros((self.max_rows, topk), dtype=torch.int64, device=dev)
+        self.rw = torch.zeros((self.max_rows, topk), dtype=torch.float16, device=dev)
+        self.xh = torch.zeros((self.max_rows, H), dtype=torch.float16, device=dev)
+        self.y = torch.zeros((self.max_rows, H), dtype=torch.float32, device=dev)     # fp32 accumulator, kept zeroed
+        self.out = torch.zeros((self.max_rows, H), dtype=torch.bfloat16, device=dev)
+        self.scr = moe4.scratch(dev)
+        self._pf = None
+
+    # ---- routing ---------------------------------------------------------------------------------------------
+    def route(self, x, write_xh=True):
+        R = x.shape[0]
+        router.router_fused(x, self.wg, self.bias, self.logits, self.ctr, self.sel[:R], self.rw[:R], self.topk,
+                            self.scale, self.xh[:R] if write_xh else None)
+        return self.sel[:R], self.rw[:R]
+
+    # ---- decode ----------------------------------------------------------------------------------------------
+    def experts_decode(self, R, y, with_shared=True, blocks=0):
+        """moe4.forward on the routed selection (and the shared expert) of self.xh[:R], added into y"""
+        gq, uq, dq, gs, us, ds = self.bank.tables()
+        sh = self.shared if (with_shared and self.shared is not None) else (0, 0, 0)
+        moe4.forward(self.xh[:R], self.sel[:R], self.rw[:R], self.n_hot, gq, uq, dq, gs, us, ds, *self.scr, y, blocks,
+                     0, self.lo, sh[0], sh[1], sh[2], 0, 0, 0, xf=1)
+
+    def decode(self, x):
+        """the decode layer: bf16 [R, H] out (router + routed + shared)"""
+        R = x.shape[0]
+        self.route(x)
+        self.experts_decode(R, self.y[:R])
+        return moe4.finish_bf16(self.y[:R], R, self.out[:R])
+
+    # ---- prefill ----------------------------------------------------------------------------------------------
+    def _prefill_buffers(self, T):
+        if self._pf is not None and self._pf.T >= T:
+            return self._pf
+        self._pf = PrefillBuffers(T, self.topk, self.lo, self.n_hot, self.E, self.device)
+        return self._pf
+
+    def prefill_experts(self, x, y, with_shared=True):
+        """routed (+ shared) experts of x's routed selection (in the prefill buffers) added into y fp32 [T, H]"""
+        T = x.shape[0]
+        pf = self._pf
+        gq, uq, dq, gs, us, ds = self.bank.tables()
+        sh = self.shared if (with_shared and self.shared is not None) else None
+        moe4p.forward(x, pf.tok, pf.eid, pf.wt, pf.rbt, gq, uq, dq, gs, us, ds, *pf.scr, y,
+                      inv=pf.inv[:T * self.topk], meta=pf.meta, topk=self.topk, shared=sh, npos=pf.F, nrb=pf.nrb_max)
+
+    def prefill(self, x, with_shared=True):
+        """the prefill layer: bf16 [T, H] out (router, device dispatch plan, grouped GEMMs, per-token combine)"""
+        T = x.shape[0]
+        pf = self._prefill_buffers(T)
+        sel, rw = pf.sel[:T], pf.rw[:T]
+        router.router_fused(x, self.wg, self.bias, pf.logits, self.ctr, sel, rw, self.topk, self.scale)
+        pf.run(sel, rw)
+        y = pf.y[:T]
+        self.prefill_experts(x, y, with_shared)
+        return moe4.finish_bf16(y, T, pf.out[:T])
+
+    def forward(self, x):
+        return self.decode(x) if x.shape[0] <= 16 else self.prefill(x)

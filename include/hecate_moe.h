@@ -1,0 +1,145 @@
+/* hecate_moe.h - C ABI of the MI355X (gfx950) routed int4 MoE hot path: the drop-in for chronarion/hecate's GPU-tier
+ * MoE operators (runtime/tier/moe4/moe4.cu, moe4p.cu, runtime/core/exl3_router.py).
+ *
+ * Conventions (kept from the reference's pybind ops, runtime/tier/moe4/moe4.cu:826-843):
+ *   - every pointer is a device address unless the argument name ends in _host; sizes are plain ints;
+ *   - expert weights are passed as int64 device tables of raw device addresses, one table per matrix and per scale
+ *     (runtime/tier/tier_split.py:206-214, 246); the caller owns every buffer, the library never frees;
+ *   - work is queued on `stream` (a hipStream_t; NULL = default stream), asynchronously, with a static launch shape
+ *     and no allocation, host synchronisation or hipMemset, so the launches are hipGraph-capturable;
+ *   - scratch buffers come back zeroed (self-cleaning) and calls that share one scratch must not overlap;
+ *   - every entry point returns HMOE_OK or an error code; hmoe_last_error() gives the thread's last message.
+ *
+ * Formats (this build's gfx950 layouts, hmoe_pack_* produce them from the canonical row-major ones):
+ *   I4G128 int4 matrix [N][K] (N % 16 == 0, K % 128 == 0): codes in 1 KB tiles of 16 rows x 128 k, tile (nb, kg) at
+ *          byte (nb * K/128 + kg) * 1024; lane l (0..63) of a tile holds 16 bytes = 4 dwords, dword j packs the 8 codes
+ *          (q + 8) of row nb*16 + l%16 at k = kg*128 + 32j + 8(l/16) + e, e = 0..7, code e at bit 4(e/2) + 16(e%2).
+ *          Scales bf16 [N/16][K/128][16]: the 16 row scales of tile (nb, kg), contiguous.
+ *   F16T   dense matrix [N][K] (K % 32 == 0) as f16 in 1 KB tiles of 16 rows x 32 k, tile (nb, ks) at byte
+ *          (nb * K/32 + ks) * 1024, lane l holds the 8 f16 of row nb*16 + l%16 at k = ks*32 + 8(l/16) + e.
+ *   x      bf16 [R][H] (the MoE input); xh its f16 copy (exact for the reference's fp16 activation range).
+ */
+#ifndef HECATE_MOE_H
+#define HECATE_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HMOE_H 6144            /* hidden size (runtime/tier/moe4/moe4.cu:33) */
+#define HMOE_I 2048            /* expert intermediate size */
+#define HMOE_TOPK 8
+#define HMOE_MAXR 16           /* decode rows per call (the reference's MAXR is 8; 8 requests + 8 draft rows need 16) */
+#define HMOE_MAXE 256          /* expert ids per residency window */
+#define HMOE_MAXSLOT 128       /* distinct experts per decode call (MAXR * TOPK) */
+
+enum { HMOE_OK = 0, HMOE_ERR_ARG = 1, HMOE_ERR_HIP = 2 };
+
+/* last error message of the calling thread ("" if none) */
+const char* hmoe_last_error(void);
+/* ABI version of this library */
+int hmoe_version(void);
+
+/* ---- formats (host) ------------------------------------------------------------------------------------------ */
+/* canonical int4 (codes uint8 [N][K/2], code = q + 8, low nibble = even k, as runtime/tier/cpuband.cpp:3-4 and
+ * tier_split.py:104-106; scales bf16 [N][K/128]) -> I4G128. Replaces the reference's pack_u4
+ * (tools/quant/gptq_int4.py:74-77) for this build's layout. */
+int hmoe_pack_i4(const uint8_t* codes_host, const uint16_t* scales_host, int N, int K, void* q_host, void* s_host);
+/* inverse of hmoe_pack_i4 (tier_split.py:98-101 _unpack_moe4 is the reference's inverse of its own packing) */
+int hmoe_unpack_i4(const void* q_host, const void* s_host, int N, int K, uint8_t* codes_host, uint16_t* scales_host);
+/* dense bf16 [N][K] -> F16T (the shared expert; bf16 -> f16 is exact for |w| in [2^-14, 65504]) */
+int hmoe_pack_dense(const uint16_t* w_bf16_host, int N, int K, uint16_t* f16t_host);
+/* the reference's moe4 weights (fragment-order int4, tools/quant/gptq_int4.py:74-77, with fp32 row scales,
+ * tier_split.py:207-214) -> I4G128 with the row scale rounded to bf16 in every group */
+int hmoe_repack_moe4(const uint8_t* frag_q_host, const float* row_scale_host, int N, int K, void* q_host, void* s_host);
+
+/* ---- synthetic data on the device (include/hmoe_rng.h; no reference counterpart: seeded benchmark weights) ---- */
+int hmoe_gen_i4(uint64_t key_q, uint64_t key_s, float sigma_s, int N, int K, void* q, void* s, void* stream);
+int hmoe_gen_dense(uint64_t key, float sigma, int N, int K, void* f16t, void* stream);
+/* out[i] = mean + sigma * z(key, i); dtype 0 = fp32, 1 = bf16 */
+int hmoe_gen_normal(uint64_t key, int64_t n, float mean, float sigma, int dtype, void* out, void* stream);
+
+/* ---- router: runtime/core/exl3_router.py:134-146 router_fused(x, wt, bias, logits, ctr, sel, rw, topk, scale) ----
+ * x bf16 [R][K]; wt fp32 [E][K] (the transposed gate); bias fp32 [E] or NULL (selection only); logits fp32 scratch
+ * of hmoe_router_scratch_bytes(R, E) bytes; ctr int32 [1] zero (self-resetting); sel int64 [R][topk]; rw f16
+ * [R][topk] = f16(a * scale / (sum a + 1e-20)); xh optional f16 [R][K] copy of x for hmoe_moe4_forward(xf = 1).
+ * Logits in fp32 with one fixed summation order (bit-reproducible): 8 segments of K/8, each the in-order sum from 0
+ * of 32-element fmaf chains (k ascending, from 0), the segment sums added in order from 0. Sigmoid, keys and weights
+ * follow exl3_router.py:94-127 with the exp of include/hmoe_rng.h. R >= 1, E <= 256, topk <= 8, K % 256 == 0. */
+size_t hmoe_router_scratch_bytes(int R, int E);
+int hmoe_router_fused(const void* x, const float* wt, const float* bias, float* logits, int* ctr, int64_t* sel,
+                      uint16_t* rw, int R, int K, int E, int topk, float scale, void* xh, void* stream);
+
+/* ---- decode: runtime/tier/moe4/moe4.cu:828-895 moe4_forward ----
+ * x [R][H] bf16 (xf = 0) or its f16 copy (xf = 1, as the router writes it); sel int64 [R][8]; rw f16 [R][8];
+ * picks with sel - lo in [0, n_hot) run, tables indexed by sel - lo hold I4G128 codes (gate/up [I][H], down [H][I])
+ * and their scales; y fp32 [R][H] is accumulated into. sh_gw / sh_uw / sh_dw: the shared expert as F16T (gate/up
+ * [I][H], down [H][I]) or NULL; sh_gs / sh_us / sh_ds must be NULL (the reference's int8 row scales; F16T has none).
+ * Scratch (act, gu32, ctr_a, y32, ctr_b) from hmoe_moe4_scratch_bytes, zeroed once. blocks: persistent grid size
+ * (0 = default), blocks_a: unused (kept for the reference's argument position). R in [1, 16]. */
+size_t hmoe_moe4_scratch_bytes(int which);      /* which: 0 act, 1 gu32, 2 ctr_a, 3 y32, 4 ctr_b */
+int hmoe_moe4_forward(const void* x, const int64_t* sel, const uint16_t* rw, int R, int n_hot,
+                      const int64_t* gate_w, const int64_t* up_w, const int64_t* down_w,
+                      const int64_t* gate_s, const int64_t* up_s, const int64_t* down_s,
+                      void* act, float* gu32, int* ctr_a, float* y32, int* ctr_b, float* y, int blocks, int blocks_a,
+                      int lo, const void* sh_gw, const void* sh_uw, const void* sh_dw, const void* sh_gs,
+                      const void* sh_us, const void* sh_ds, int xf, void* stream);
+/* the two phases of hmoe_moe4_forward, for callers that time or schedule them apart (this build's addition):
+ * gate_up writes act (and the f16 copy of x when xf = 0), down adds into y; same arguments and rules as forward */
+int hmoe_moe4_gate_up(const void* x, const int64_t* sel, const uint16_t* rw, int R, int n_hot,
+                      const int64_t* gate_w, const int64_t* up_w, const int64_t* gate_s, const int64_t* up_s,
+                      void* act, float* gu32, int* ctr_a, int blocks, int lo, const void* sh_gw, const void* sh_uw,
+                      int xf, void* stream);
+int hmoe_moe4_down(const int64_t* sel, const uint16_t* rw, int R, int n_hot, const int64_t* down_w,
+                   const int64_t* down_s, const void* act, float* y32, int* ctr_b, float* y, int blocks, int lo,
+                   const void* sh_dw, void* stream);
+/* moe4.cu:700-717,817-824: f[r] += y[r] (+ o[r]) (+ o2[r]) in that order, y zeroed; o, o2 may be NULL. done must be
+ * NULL (the cross-device DONE flag is out of scope). f, y fp32 [rows][H]. */
+int hmoe_moe4_combine(float* f, const float* o, float* y, int rows, const float* o2, const unsigned* done, void* stream);
+/* moe4.cu:678-698,904-911: I4G128 codes + scales -> f16 [N][K] (value (q) * scale, rounded to f16) */
+int hmoe_moe4_dequant(const void* q, const void* s, int N, int K, uint16_t* out, void* stream);
+/* y fp32 [rows][H] -> bf16 out (the layer output), y zeroed (the combine's self-cleaning, this build's addition) */
+int hmoe_finish_bf16(float* y, int rows, uint16_t* out, void* stream);
+
+/* ---- prefill dispatch: runtime/tier/tier_split.py:400-420 (argsort, bincount, tok/eid/wt) and
+ * runtime/tier/rtx_split.py:236-255 (pick_groups) on the device, with no host sync ----
+ * sel int64 [T][topk], rw f16 [T][topk]; window [lo, lo + n). Outputs: counts int32 [n], tok/eid int32 [T*topk],
+ * wt fp32 [T*topk], inv int32 [T*topk] (position of each flat pick, -1 outside the window), rbt int32 [nrb_max][4]
+ * rows {expert, first pick, picks, 0} with bm rows per block (balance as pick_groups), meta int32 [4] = {npos, nrb,
+ * 0, 0}. work: scratch of hmoe_dispatch_work_bytes(T, topk, n) bytes. nrb_max = hmoe_dispatch_nrb_max(T*topk, n, bm). */
+size_t hmoe_dispatch_work_bytes(int T, int topk, int n);
+int hmoe_dispatch_nrb_max(int npos_max, int n, int bm);
+int hmoe_dispatch(const int64_t* sel, const uint16_t* rw, int T, int topk, int lo, int n, int bm, int balance,
+                  int* counts, int* tok, int* eid, float* wt, int* inv, int* rbt, int nrb_max, int* meta, void* work,
+                  void* stream);
+
+/* ---- prefill: runtime/tier/moe4/moe4p.cu:217-245 moe4p_forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar,
+ * d, out) ----
+ * x bf16 [T][H]; tok int32 [npos] (token of each pick), eid int32 [npos] (not read: the expert of a row block is in
+ * rbt), wt fp32 [npos]; rbt int32 [nrb][4] rows {expert (relative to the tables), first pick, picks <= 64, 0};
+ * tables (n_tab entries) as in hmoe_moe4_forward; ar f16 [ps + T][I] and d fp32 [ps + T][H] scratch
+ * (hmoe_moe4p_scratch_bytes); gu unused (NULL allowed); out fp32 [T][H] accumulated into. meta: NULL, or the device
+ * {npos, nrb} written by hmoe_dispatch (then npos / nrb are the static maxima the grids are sized for). inv: NULL
+ * (picks added with atomics, as p4_fin_kernel) or the dispatch's inverse map (each token's picks added in top-k
+ * order: deterministic). sh_*: the shared expert as F16T or NULL (needs inv); it runs on every token with weight 1. */
+size_t hmoe_moe4p_scratch_bytes(int which, int ps, int T);     /* which: 0 gu, 1 ar, 2 d */
+int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid, const float* wt, const int* rbt, int npos,
+                       int nrb, int n_tab, const int64_t* gw, const int64_t* uw, const int64_t* dw, const int64_t* gs,
+                       const int64_t* us, const int64_t* ds, float* gu, uint16_t* ar, float* d, float* out, int ps,
+                       const int* meta, const int* inv, int T, int topk, const void* sh_gw, const void* sh_uw,
+                       const void* sh_dw, void* stream);
+
+/* ---- residual + RMSNorm between layers: runtime/tier/cn.cu:48-103 (combine_norm) restated for fp32 weights ----
+ * r fp32 [R][H] residual += a (a fp32 [R][H] or NULL; a is zeroed after use), xn = bf16(r * rsqrt(mean r^2 + eps) * w)
+ * in one fixed fp32 order: 256 fmaf chains over k = t, t + 256, ..., folded by halving (t += t + off, off = 128..1),
+ * rmf = 1 / sqrt(sum / H + eps), xn = bf16((r * rmf) * w); xh optional f16 copy of xn. */
+int hmoe_residual_rmsnorm(float* r, float* a, const float* w, int R, float eps, uint16_t* xn, uint16_t* xh,
+                          void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
