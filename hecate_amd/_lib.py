@@ -27,6 +27,8 @@ SIGNATURES = {
                                 P, P, P, P, P, P, i32, P]),
     "hmoe_moe4_gate_up": (i32, [P, P, P, i32, i32, P, P, P, P, P, P, P, i32, i32, P, P, i32, P]),
     "hmoe_moe4_down": (i32, [P, P, i32, i32, P, P, P, P, P, P, i32, i32, P, P]),
+    "hmoe_moe_decode_layer": (i32, [P, P, P, i32, i32, f32, P, P, P, i32, i32, i32, P, P, P, P, P, P, P, P, P, P, P,
+                                    P, P, P, P, i32, i32, P]),
     "hmoe_moe4_combine": (i32, [P, P, P, i32, P, P, P]),
     "hmoe_moe4_dequant": (i32, [P, P, i32, i32, P, P]),
     "hmoe_finish_bf16": (i32, [P, i32, P, P]),

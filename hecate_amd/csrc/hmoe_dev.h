@@ -66,4 +66,117 @@ __device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*) p;
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
+// top-k of one row by a wave: keys of experts lane + 64 i; each round takes the largest (key, -index) pair, so ties
+// go to the lowest index (exl3_router.py:106-121); the sum runs over the selected unbiased activations in order
+__device__ inline void select_row(const float* __restrict__ lg, const float* __restrict__ bias, int E, int topk, float scale,
+                           int64_t* __restrict__ sel, uint16_t* __restrict__ rw)
+{
+    const int lane = threadIdx.x & 63;
+    float a[4]; uint32_t key[4];
+    #pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        const int e = lane + 64 * i;
+        if (e < E)
+        {
+            a[i] = hmoe_sigmoid(lg[e]);
+            key[i] = hmoe_okey(a[i] + (bias ? bias[e] : 0.0f));
+        }
+        else { a[i] = 0.f; key[i] = 0u; }
+    }
+    float sum = 0.f, wsel = 0.f; int isel = 0;
+    for (int k = 0; k < topk; ++k)
+    {
+        uint64_t best = 0ull;
+        #pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            const uint64_t v = ((uint64_t) key[i] << 32) | (uint32_t) (0xffffu - (lane + 64 * i));
+            best = v > best ? v : best;
+        }
+        #pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+        {
+            const uint32_t lo = __shfl_xor((uint32_t) best, off), hi = __shfl_xor((uint32_t) (best >> 32), off);
+            const uint64_t o = ((uint64_t) hi << 32) | lo;
+            best = o > best ? o : best;
+        }
+        const int e = 0xffff - (int) (best & 0xffffu);
+        float mine = 0.f;
+        if ((e & 63) == lane)
+        {
+            #pragma unroll
+            for (int i = 0; i < 4; ++i) if (i == (e >> 6)) { mine = a[i]; key[i] = 0u; }
+        }
+        const float av = __shfl(mine, e & 63);
+        sum = sum + av;
+        if (lane == k) { wsel = av; isel = e; }
+    }
+    if (lane < topk)
+    {
+        sel[lane] = isel;
+        rw[lane] = hmoe_f2h((wsel * scale) / (sum + 1e-20f));
+    }
+}
+
+
+// ---- router logits, fixed order (see hecate_moe.h) ----
+constexpr int RCHUNK = 32, RSEG = 8, RMAXE = 256;
+
+// logits of expert e for R <= 16 rows by 256 threads (tid in [0, 256)): thread c computes the fmaf chain of chunk c
+// for every row into sums[c][r]; after the workgroup barrier threads r < R fold the chunk sums in segment order and
+// write logits[r * RMAXE + e]. Every thread of the workgroup must call it (it contains a barrier). e >= E: no-op.
+__device__ inline void expert_logits(const uint16_t* __restrict__ x, const float* __restrict__ wt, int e, int E, int R,
+                                     int K, int tid, float (*sums)[MAXR + 1], float* __restrict__ logits)
+{
+    const int nch = K / RCHUNK;
+    if (e < E && tid < nch)
+    {
+        const float* w = wt + (size_t) e * K + tid * RCHUNK;
+        float wv[RCHUNK];
+        #pragma unroll
+        for (int i = 0; i < RCHUNK; i += 4)
+        {
+            const f32x4 v = *(const f32x4*) (w + i);
+            wv[i] = v[0]; wv[i + 1] = v[1]; wv[i + 2] = v[2]; wv[i + 3] = v[3];
+        }
+        for (int r = 0; r < R; ++r)
+        {
+            const uint16_t* xr = x + (size_t) r * K + tid * RCHUNK;
+            u32x4 xv[4];
+            #pragma unroll
+            for (int i = 0; i < 4; ++i) xv[i] = *(const u32x4*) (xr + 8 * i);
+            float acc = 0.f;
+            #pragma unroll
+            for (int i = 0; i < 4; ++i)
+                #pragma unroll
+                for (int k = 0; k < 4; ++k)
+                {
+                    acc = __builtin_fmaf(__uint_as_float(xv[i][k] << 16), wv[8 * i + 2 * k], acc);
+                    acc = __builtin_fmaf(__uint_as_float(xv[i][k] & 0xffff0000u), wv[8 * i + 2 * k + 1], acc);
+                }
+            sums[tid][r] = acc;
+        }
+    }
+    __syncthreads();
+    if (e < E && tid < R)
+    {
+        const int cps = nch / RSEG;
+        float t = 0.f;
+        for (int s = 0; s < RSEG; ++s)
+        {
+            float seg = 0.f;
+            for (int q = s * cps; q < (s + 1) * cps; ++q) seg = seg + sums[q][tid];
+            t = t + seg;
+        }
+        logits[(size_t) tid * RMAXE + e] = t;
+    }
+}
+
+// bf16 -> f16 of n elements [b0, b1) by the calling threads (stride nthr from tid)
+__device__ inline void to_f16_range(const uint16_t* __restrict__ x, _Float16* __restrict__ xh, int b0, int b1, int tid,
+                                    int nthr)
+{
+    for (int i = b0 + tid; i < b1; i += nthr) xh[i] = (_Float16) bf2f(x[i]);
+}
 }  // namespace hmoe

@@ -2,138 +2,39 @@
 // nr4_kernel.cuh:307-366) on gfx950, with fp32 logits in one fixed summation order so the selection is reproducible:
 // logit = sum over 8 segments (in order, from 0) of [sum over the segment's 32-element chunks (in order, from 0) of
 // a fmaf chain over the chunk's k ascending from 0].
-//   small (R <= 16): one launch. Workgroup e computes expert e's logits for every row, one chunk per thread; the
-//                    chunk sums fold through LDS; the last workgroup to finish (self-resetting counter, as
-//                    exl3_router.py:74-83,130) selects each row's top-k and writes sel / rw.
+//   small (R <= 16): a logits kernel (two experts per workgroup, one 32-element chunk per thread, chunk sums folded
+//                    through LDS) and a select kernel (one wave per row); the kernel boundary replaces the reference's
+//                    last-block counter (exl3_router.py:74-83,130), whose cross-workgroup fences are costly on gfx950.
 //   large (R > 16) : a register-tiled fp32 GEMM per (64 rows, 64 experts, segment) with the same chain order, then a
 //                    select kernel that folds the 8 segment sums and picks each row's top-k (one wave per row).
 #include "hmoe_dev.h"
 
 namespace hmoe {
 
-constexpr int RCHUNK = 32, RSEG = 8, RMAXE = 256;
 
-// top-k of one row by a wave: keys of experts lane + 64 i; each round takes the largest (key, -index) pair, so ties
-// go to the lowest index (exl3_router.py:106-121); the sum runs over the selected unbiased activations in order
-__device__ void select_row(const float* __restrict__ lg, const float* __restrict__ bias, int E, int topk, float scale,
-                           int64_t* __restrict__ sel, uint16_t* __restrict__ rw)
+// small path, 1: two experts per 512-thread workgroup (expert_logits), optional f16 copy of x
+__global__ void __launch_bounds__(512) router_logits_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ wt, float* __restrict__ logits, int R, int K, int E,
+    _Float16* __restrict__ xh)
 {
-    const int lane = threadIdx.x & 63;
-    float a[4]; uint32_t key[4];
-    #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    __shared__ float sums[2][256][MAXR + 1];
+    const int half = threadIdx.x >> 8, tid = threadIdx.x & 255;
+    expert_logits(x, wt, 2 * blockIdx.x + half, E, R, K, tid, sums[half], logits);
+    if (xh)
     {
-        const int e = lane + 64 * i;
-        if (e < E)
-        {
-            a[i] = hmoe_sigmoid(lg[e]);
-            key[i] = hmoe_okey(a[i] + (bias ? bias[e] : 0.0f));
-        }
-        else { a[i] = 0.f; key[i] = 0u; }
-    }
-    float sum = 0.f, wsel = 0.f; int isel = 0;
-    for (int k = 0; k < topk; ++k)
-    {
-        uint64_t best = 0ull;
-        #pragma unroll
-        for (int i = 0; i < 4; ++i)
-        {
-            const uint64_t v = ((uint64_t) key[i] << 32) | (uint32_t) (0xffffu - (lane + 64 * i));
-            best = v > best ? v : best;
-        }
-        #pragma unroll
-        for (int off = 32; off > 0; off >>= 1)
-        {
-            const uint32_t lo = __shfl_xor((uint32_t) best, off), hi = __shfl_xor((uint32_t) (best >> 32), off);
-            const uint64_t o = ((uint64_t) hi << 32) | lo;
-            best = o > best ? o : best;
-        }
-        const int e = 0xffff - (int) (best & 0xffffu);
-        float mine = 0.f;
-        if ((e & 63) == lane)
-        {
-            #pragma unroll
-            for (int i = 0; i < 4; ++i) if (i == (e >> 6)) { mine = a[i]; key[i] = 0u; }
-        }
-        const float av = __shfl(mine, e & 63);
-        sum = sum + av;
-        if (lane == k) { wsel = av; isel = e; }
-    }
-    if (lane < topk)
-    {
-        sel[lane] = isel;
-        rw[lane] = hmoe_f2h((wsel * scale) / (sum + 1e-20f));
+        const int n = R * K, per = (n + gridDim.x - 1) / gridDim.x, b0 = blockIdx.x * per;
+        to_f16_range(x, xh, b0, min(n, b0 + per), threadIdx.x, blockDim.x);
     }
 }
 
-// small path: blockIdx.x = expert, thread c = chunk (K / 32 chunks <= blockDim), every row
-__global__ void __launch_bounds__(256) router_small_kernel(
-    const uint16_t* __restrict__ x, const float* __restrict__ wt, const float* __restrict__ bias,
-    float* __restrict__ logits, int* __restrict__ ctr, int64_t* __restrict__ sel, uint16_t* __restrict__ rw, int R,
-    int K, int E, int topk, float scale, _Float16* __restrict__ xh)
+// small path, 2: one wave per row selects the top-k from the finished logits
+__global__ void __launch_bounds__(1024) router_select_small_kernel(const float* __restrict__ logits,
+    const float* __restrict__ bias, int R, int E, int topk, float scale, int64_t* __restrict__ sel,
+    uint16_t* __restrict__ rw)
 {
-    __shared__ float sums[256][MAXR + 1];
-    __shared__ int s_last;
-    const int e = blockIdx.x, c = threadIdx.x, nch = K / RCHUNK;
-    if (c < nch)
-    {
-        const float* w = wt + (size_t) e * K + c * RCHUNK;
-        float wv[RCHUNK];
-        #pragma unroll
-        for (int i = 0; i < RCHUNK; i += 4) { const f32x4 v = *(const f32x4*) (w + i); wv[i] = v[0]; wv[i + 1] = v[1]; wv[i + 2] = v[2]; wv[i + 3] = v[3]; }
-        for (int r = 0; r < R; ++r)
-        {
-            const uint16_t* xr = x + (size_t) r * K + c * RCHUNK;
-            float acc = 0.f;
-            #pragma unroll
-            for (int i = 0; i < RCHUNK; i += 8)
-            {
-                const u32x4 v = *(const u32x4*) (xr + i);
-                #pragma unroll
-                for (int k = 0; k < 4; ++k)
-                {
-                    acc = __builtin_fmaf(__uint_as_float(v[k] << 16), wv[i + 2 * k], acc);
-                    acc = __builtin_fmaf(__uint_as_float(v[k] & 0xffff0000u), wv[i + 2 * k + 1], acc);
-                }
-            }
-            sums[c][r] = acc;
-        }
-    }
-    // the f16 copy of x for the decode kernels: this workgroup's slice
-    if (xh)
-    {
-        const int n = R * K, per = (n + gridDim.x - 1) / gridDim.x, b0 = e * per, b1 = min(n, b0 + per);
-        for (int i = b0 + c; i < b1; i += blockDim.x) xh[i] = (_Float16) bf2f(x[i]);
-    }
-    __syncthreads();
-    if (c < R)
-    {
-        const int cps = nch / RSEG;
-        float t = 0.f;
-        for (int s = 0; s < RSEG; ++s)
-        {
-            float seg = 0.f;
-            for (int q = s * cps; q < (s + 1) * cps; ++q) seg = seg + sums[q][c];
-            t = t + seg;
-        }
-        logits[(size_t) c * RMAXE + e] = t;
-    }
-    __threadfence();
-    __syncthreads();
-    if (c == 0) s_last = atomicAdd(ctr, 1) == (int) gridDim.x - 1;
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const int wave = c >> 6, nw = blockDim.x >> 6;
-    for (int r = wave; r < R; r += nw)
-    {
-        float* lg = logits + (size_t) r * RMAXE;
-        // coherent reads of the other workgroups' logits
-        __shared__ float lrow[4][RMAXE];
-        for (int i = c & 63; i < E; i += 64) lrow[wave][i] = __hip_atomic_load(lg + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        select_row(lrow[wave], bias, E, topk, scale, sel + (size_t) r * topk, rw + (size_t) r * topk);
-    }
-    if (c == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int r = threadIdx.x >> 6;
+    if (r >= R) return;
+    select_row(logits + (size_t) r * RMAXE, bias, E, topk, scale, sel + (size_t) r * topk, rw + (size_t) r * topk);
 }
 
 // large path, 1: segment sums seg[s][r][e] for a 64-row x 64-expert tile, 4 x 4 outputs per thread
@@ -248,7 +149,8 @@ extern "C" int hmoe_router_fused(const void* x, const float* wt, const float* bi
                                  int64_t* sel, uint16_t* rw, int R, int K, int E, int topk, float scale, void* xh,
                                  void* stream)
 {
-    HMOE_REQUIRE(x && wt && logits && ctr && sel && rw, "router_fused: null buffer");
+    HMOE_REQUIRE(x && wt && logits && sel && rw, "router_fused: null buffer");
+    (void) ctr;
     HMOE_REQUIRE(R >= 1 && E >= 1 && E <= RMAXE && topk >= 1 && topk <= TOPK && topk <= E,
                  "router_fused: rows %d experts %d topk %d", R, E, topk);
     HMOE_REQUIRE(K > 0 && K % (RCHUNK * RSEG) == 0 && K / RCHUNK <= 256, "router_fused: K %d", K);
@@ -256,8 +158,8 @@ extern "C" int hmoe_router_fused(const void* x, const float* wt, const float* bi
     hipStream_t st = (hipStream_t) stream;
     if (R <= MAXR)
     {
-        router_small_kernel<<<E, 256, 0, st>>>((const uint16_t*) x, wt, bias, logits, ctr, sel, rw, R, K, E, topk, scale,
-                                               (_Float16*) xh);
+        router_logits_kernel<<<(E + 1) / 2, 512, 0, st>>>((const uint16_t*) x, wt, logits, R, K, E, (_Float16*) xh);
+        router_select_small_kernel<<<1, 1024, 0, st>>>(logits, bias, R, E, topk, scale, sel, rw);
         return HMOE_LAUNCHED("router_fused");
     }
     dim3 g((R + 63) / 64, (E + 63) / 64, RSEG);

@@ -52,6 +52,19 @@ def forward(x, sel, rw, n_hot, gate_w, up_w, down_w, gate_s, up_s, down_s, act, 
          _addr(sh_ds), int(xf), stream_of(x.device))
 
 
+def gate_up(x, sel, rw, n_hot, gate_w, up_w, gate_s, up_s, act, gu32, ctr_a, blocks, lo, sh_gw=0, sh_uw=0, xf=0):
+    """phase 1 of forward: act of the routed experts (and the shared expert)"""
+    call("hmoe_moe4_gate_up", ptr(x), ptr(sel), ptr(rw), x.shape[0], int(n_hot), ptr(gate_w), ptr(up_w), ptr(gate_s),
+         ptr(up_s), ptr(act), ptr(gu32), ptr(ctr_a), int(blocks), int(lo), _addr(sh_gw), _addr(sh_uw), int(xf),
+         stream_of(x.device))
+
+
+def down(sel, rw, n_hot, down_w, down_s, act, y32, ctr_b, y, blocks, lo, sh_dw=0):
+    """phase 2 of forward: y += down projections of act"""
+    call("hmoe_moe4_down", ptr(sel), ptr(rw), sel.shape[0], int(n_hot), ptr(down_w), ptr(down_s), ptr(act), ptr(y32),
+         ptr(ctr_b), ptr(y), int(blocks), int(lo), _addr(sh_dw), stream_of(y.device))
+
+
 def combine(f, o_ptr, y, rows, o2_ptr=0, done_ptr=0):
     """moe4.cu:817-824: f += y (+ o) (+ o2); y = 0"""
     _req(f.is_contiguous() and f.shape[-1] == H and f.dtype == torch.float32, "f")

@@ -139,19 +139,40 @@ class MoELayer:
         return self.sel[:R], self.rw[:R]
 
     # ---- decode ----------------------------------------------------------------------------------------------
-    def experts_decode(self, R, y, with_shared=True, blocks=0):
-        """moe4.forward on the routed selection (and the shared expert) of self.xh[:R], added into y"""
+    def experts_decode(self, R, y, with_shared=True, blocks=0, xh=None, events=None):
+        """moe4.forward on the routed selection (and the shared expert) of xh (default self.xh)[:R], added into y;
+        events: three torch.cuda.Events recorded before gate/up, between the phases and after down"""
         gq, uq, dq, gs, us, ds = self.bank.tables()
         sh = self.shared if (with_shared and self.shared is not None) else (0, 0, 0)
-        moe4.forward(self.xh[:R], self.sel[:R], self.rw[:R], self.n_hot, gq, uq, dq, gs, us, ds, *self.scr, y, blocks,
-                     0, self.lo, sh[0], sh[1], sh[2], 0, 0, 0, xf=1)
+        xh = self.xh if xh is None else xh
+        if events is None:
+            moe4.forward(xh[:R], self.sel[:R], self.rw[:R], self.n_hot, gq, uq, dq, gs, us, ds, *self.scr, y, blocks,
+                         0, self.lo, sh[0], sh[1], sh[2], 0, 0, 0, xf=1)
+            return
+        act, gu32, ctr_a, y32, ctr_b = self.scr
+        events[0].record()
+        moe4.gate_up(xh[:R], self.sel[:R], self.rw[:R], self.n_hot, gq, uq, gs, us, act, gu32, ctr_a, blocks, self.lo,
+                     sh[0], sh[1], xf=1)
+        events[1].record()
+        moe4.down(self.sel[:R], self.rw[:R], self.n_hot, dq, ds, act, y32, ctr_b, y, blocks, self.lo, sh[2])
+        events[2].record()
 
-    def decode(self, x):
-        """the decode layer: bf16 [R, H] out (router + routed + shared)"""
+    def decode(self, x, y=None, out=True, with_shared=True, phases=15, blocks=0):
+        """the decode layer in four launches (hmoe_moe_decode_layer): router + routed + shared experts of x bf16
+        [R, H]; returns the bf16 [R, H] output (out=True) and / or adds into the fp32 y. phases: bit mask of the
+        launches (1 router + shared gate/up, 2 routed gate/up, 4 down, 8 output) for callers that time them apart"""
         R = x.shape[0]
-        self.route(x)
-        self.experts_decode(R, self.y[:R])
-        return moe4.finish_bf16(self.y[:R], R, self.out[:R])
+        if not (1 <= R <= 16 and x.dtype == torch.bfloat16 and x.is_contiguous() and x.shape[1] == H):
+            raise RuntimeError("decode: x must be contiguous bf16 [R <= 16, 6144]")
+        gq, uq, dq, gs, us, ds = self.bank.tables()
+        sh = self.shared if (with_shared and self.shared is not None) else (None, None, None)
+        act, gu32, ctr_a, y32, _ = self.scr
+        o = self.out[:R] if out else None
+        call("hmoe_moe_decode_layer", ptr(x), ptr(self.wg), ptr(self.bias), self.E, self.topk, float(self.scale),
+             ptr(self.logits), ptr(self.sel), ptr(self.rw), R, self.n_hot, self.lo, ptr(gq), ptr(uq), ptr(dq), ptr(gs),
+             ptr(us), ptr(ds), ptr(sh[0]), ptr(sh[1]), ptr(sh[2]), ptr(act), ptr(gu32), ptr(ctr_a), ptr(y32),
+             ptr(y), ptr(o), int(blocks), int(phases), stream_of(x.device))
+        return o
 
     # ---- prefill ----------------------------------------------------------------------------------------------
     def _prefill_buffers(self, T):

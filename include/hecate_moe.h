@@ -64,7 +64,7 @@ int hmoe_gen_normal(uint64_t key, int64_t n, float mean, float sigma, int dtype,
 
 /* ---- router: runtime/core/exl3_router.py:134-146 router_fused(x, wt, bias, logits, ctr, sel, rw, topk, scale) ----
  * x bf16 [R][K]; wt fp32 [E][K] (the transposed gate); bias fp32 [E] or NULL (selection only); logits fp32 scratch
- * of hmoe_router_scratch_bytes(R, E) bytes; ctr int32 [1] zero (self-resetting); sel int64 [R][topk]; rw f16
+ * of hmoe_router_scratch_bytes(R, E) bytes; ctr unused (kept for the argument position); sel int64 [R][topk]; rw f16
  * [R][topk] = f16(a * scale / (sum a + 1e-20)); xh optional f16 [R][K] copy of x for hmoe_moe4_forward(xf = 1).
  * Logits in fp32 with one fixed summation order (bit-reproducible): 8 segments of K/8, each the in-order sum from 0
  * of 32-element fmaf chains (k ascending, from 0), the segment sums added in order from 0. Sigmoid, keys and weights
@@ -78,8 +78,9 @@ int hmoe_router_fused(const void* x, const float* wt, const float* bias, float* 
  * picks with sel - lo in [0, n_hot) run, tables indexed by sel - lo hold I4G128 codes (gate/up [I][H], down [H][I])
  * and their scales; y fp32 [R][H] is accumulated into. sh_gw / sh_uw / sh_dw: the shared expert as F16T (gate/up
  * [I][H], down [H][I]) or NULL; sh_gs / sh_us / sh_ds must be NULL (the reference's int8 row scales; F16T has none).
- * Scratch (act, gu32, ctr_a, y32, ctr_b) from hmoe_moe4_scratch_bytes, zeroed once. blocks: persistent grid size
- * (0 = default), blocks_a: unused (kept for the reference's argument position). R in [1, 16]. */
+ * Scratch (act, gu32, ctr_a, y32, ctr_b) from hmoe_moe4_scratch_bytes (ctr_b unused). blocks: grid size of the
+ * gate/up and down kernels (0 = 2 per CU), blocks_a: unused (kept for the reference's argument position).
+ * R in [1, 16]. */
 size_t hmoe_moe4_scratch_bytes(int which);      /* which: 0 act, 1 gu32, 2 ctr_a, 3 y32, 4 ctr_b */
 int hmoe_moe4_forward(const void* x, const int64_t* sel, const uint16_t* rw, int R, int n_hot,
                       const int64_t* gate_w, const int64_t* up_w, const int64_t* down_w,
@@ -88,7 +89,8 @@ int hmoe_moe4_forward(const void* x, const int64_t* sel, const uint16_t* rw, int
                       int lo, const void* sh_gw, const void* sh_uw, const void* sh_dw, const void* sh_gs,
                       const void* sh_us, const void* sh_ds, int xf, void* stream);
 /* the two phases of hmoe_moe4_forward, for callers that time or schedule them apart (this build's addition):
- * gate_up writes act (and the f16 copy of x when xf = 0), down adds into y; same arguments and rules as forward */
+ * gate_up writes act (and the f16 copy of x when xf = 0), down adds into y (ctr_b carries its part count); same
+ * arguments and rules as forward */
 int hmoe_moe4_gate_up(const void* x, const int64_t* sel, const uint16_t* rw, int R, int n_hot,
                       const int64_t* gate_w, const int64_t* up_w, const int64_t* gate_s, const int64_t* up_s,
                       void* act, float* gu32, int* ctr_a, int blocks, int lo, const void* sh_gw, const void* sh_uw,
@@ -96,6 +98,18 @@ int hmoe_moe4_gate_up(const void* x, const int64_t* sel, const uint16_t* rw, int
 int hmoe_moe4_down(const int64_t* sel, const uint16_t* rw, int R, int n_hot, const int64_t* down_w,
                    const int64_t* down_s, const void* act, float* y32, int* ctr_b, float* y, int blocks, int lo,
                    const void* sh_dw, void* stream);
+/* the whole decode layer in the four launches of forward (this build's addition; tier_split.py:520-574 runs the
+ * router, the shared expert and moe4 apart): router logits (wt fp32 [E][H], bias) with the router_fused rules, the
+ * selection written to sel / rw (int64 / f16 [R][8]), routed experts of the picks in [lo, lo + n_hot) and the shared
+ * expert (F16T or NULL); y fp32 [R][H] accumulated into and / or out bf16 [R][H] written (either may be NULL, not
+ * both). x bf16 [R][H]. phases: bit mask of the four launches (1 router logits + shared gate/up, 2 routed gate/up,
+ * 4 down, 8 output), 15 = the whole layer. topk must be 8. */
+int hmoe_moe_decode_layer(const void* x, const float* wt, const float* bias, int E, int topk, float scale,
+                          float* logits, int64_t* sel, uint16_t* rw, int R, int n_hot, int lo,
+                          const int64_t* gate_w, const int64_t* up_w, const int64_t* down_w,
+                          const int64_t* gate_s, const int64_t* up_s, const int64_t* down_s,
+                          const void* sh_gw, const void* sh_uw, const void* sh_dw, void* act, float* gu32,
+                          int* ctr_a, float* y32, float* y, uint16_t* out, int blocks, int phases, void* stream);
 /* moe4.cu:700-717,817-824: f[r] += y[r] (+ o[r]) (+ o2[r]) in that order, y zeroed; o, o2 may be NULL. done must be
  * NULL (the cross-device DONE flag is out of scope). f, y fp32 [rows][H]. */
 int hmoe_moe4_combine(float* f, const float* o, float* y, int rows, const float* o2, const unsigned* done, void* stream);

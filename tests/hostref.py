@@ -1,67 +1,2 @@
-"""Host (numpy) copies of the synthetic layers, regenerated by the oracle's generator from the same keys the device
-uses, and the oracle's view of a layer. Test helper only."""
-import numpy as np
-
-import pyoracle as O
-from hecate_amd import synth
-
-H, I, E = 6144, 2048, 256
-
-
-class HostLayer:
-    def __init__(self, layer, seed=synth.SEED, bias_sigma=0.01, bias=None, perm=None, n_hot=E, shared=True):
-        self.layer, self.seed = layer, seed
-        k = lambda kind, e=0: synth.key(seed, layer, synth.KIND[kind], e)
-        wg = O.normal_f32(k("ROUTER"), E * H, 0.0, synth.SIG_ROUTER).reshape(E, H)
-        b = O.normal_f32(k("BIAS"), E, 0.0, bias_sigma) if bias is None else np.asarray(bias, np.float32)
-        self.perm = list(range(E)) if perm is None else list(perm)
-        p = np.array(self.perm)
-        self.wg = np.ascontiguousarray(wg[p])
-        self.bias = np.ascontiguousarray(b[p])
-        self.n_hot = n_hot
-        self._k = k
-        self._experts = {}
-        self.shared = None
-        if shared:
-            self.shared = (O.normal_bf16(k("SH_GATE"), I * H, synth.SIG_SHARED).reshape(I, H),
-                           O.normal_bf16(k("SH_UP"), I * H, synth.SIG_SHARED).reshape(I, H),
-                           O.normal_bf16(k("SH_DOWN"), H * I, synth.SIG_SHARED).reshape(H, I))
-
-    def expert(self, local):
-        """canonical int4 codes + bf16 g128 scales of local expert id `local` (original id perm[local])"""
-        if local not in self._experts:
-            e = self.perm[local]
-            k = self._k
-            self._experts[local] = {
-                "gate_q": O.codes(k("GATE_Q", e), I, H), "gate_s": O.scales(k("GATE_S", e), I, H, synth.SIG_SCALE),
-                "up_q": O.codes(k("UP_Q", e), I, H), "up_s": O.scales(k("UP_S", e), I, H, synth.SIG_SCALE),
-                "down_q": O.codes(k("DOWN_Q", e), H, I), "down_s": O.scales(k("DOWN_S", e), H, I, synth.SIG_SCALE)}
-        return self._experts[local]
-
-    def table(self, sel, lo=0):
-        """ExpertTable with the experts the selection touches inside [lo, lo + n_hot)"""
-        need = sorted({int(s) - lo for s in np.asarray(sel).ravel() if 0 <= int(s) - lo < self.n_hot})
-        ex = [None] * self.n_hot
-        for e in need:
-            ex[e] = self.expert(e)
-        return O.ExpertTable(ex)
-
-    def route(self, x_bf16):
-        return O.router(x_bf16, self.wg, self.bias)
-
-    def moe(self, x_bf16, sel, rw, mode=0, shared=True, out=None, accumulate=False, threads=16):
-        return O.moe(mode, x_bf16, sel, rw, self.table(sel), 0, self.n_hot, self.shared if shared else None,
-                     out=out, accumulate=accumulate, threads=threads)
-
-
-def x_rows(tag, R, seed=synth.SEED, layer=0):
-    return O.normal_bf16(synth.key(seed, layer, synth.KIND["X"], tag), R * H, 1.0).reshape(R, H)
-
-
-def parity(got, ref):
-    """(max |d|, mean |d| / mean |ref|)"""
-    d = np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64))
-    return float(d.max()), float(d.mean() / max(np.abs(ref).mean(), 1e-30))
-
-
-MAX_ABS, MEAN_REL = 2e-2, 5e-3      # the layer-output tolerance against the oracle's exact (fp32-activation) mode
+"""re-export of the oracle's host-layer helpers for the tests"""
+from hostlayer import HostLayer, x_rows, parity, MAX_ABS, MEAN_REL, H, I, E  # noqa: F401

@@ -9,6 +9,7 @@ import torch
 
 import pyoracle as O
 from hecate_amd import moe4, moe4p, router, synth, tier
+from hecate_amd.stack import DecodeStack
 from hecate_amd._lib import call, ptr
 from hostref import HostLayer, x_rows, parity, MAX_ABS, MEAN_REL, H, I, E
 
@@ -78,12 +79,11 @@ def test_router_bit_exact(dev, R, bias_sigma):
     logits, ctr = router.buffers(R, dev)
     sel = torch.empty((R, 8), dtype=torch.int64, device=dev); rw = torch.empty((R, 8), dtype=torch.float16, device=dev)
     xh = torch.empty((R, H), dtype=torch.float16, device=dev)
-    for _ in range(2):                       # the counter resets itself
+    for _ in range(2):                       # repeated calls on the same scratch
         router.router_fused(xt, wg, b, logits, ctr, sel, rw, 8, 2.5, xh)
     torch.cuda.synchronize()
     assert np.array_equal(sel.cpu().numpy(), sel_ref)
     assert np.array_equal(u16(rw), rw_ref)
-    assert int(ctr.item()) == 0
     assert np.array_equal(u16(xh), O.f32_to_f16(O.bf16_to_f32(x)))
 
 
@@ -125,10 +125,9 @@ def test_decode_layer_parity(dev, R):
     ma, mr = parity(y, ref)
     log(f"  max|d| {ma:.3e} mean-rel {mr:.3e}")
     assert ma <= MAX_ABS and mr <= MEAN_REL
-    # bit-reproducible and self-cleaning: a second call gives the same bits
+    # bit-reproducible: a second call (same scratch) gives the same bits
     y2 = decode_fp32(lay, x, dev).cpu().numpy()
     assert np.array_equal(y, y2)
-    assert int(lay.scr[2].abs().sum().item()) == 0 and int(lay.scr[4].abs().sum().item()) == 0
 
 
 def test_decode_zipf_16(dev):
@@ -171,6 +170,68 @@ def test_partial_resident_176(dev, R):
     lay.experts_decode(R, y0, False)
     torch.cuda.synchronize()
     assert torch.equal(y0, p0)
+
+
+@pytest.mark.parametrize("R", [1, 16])
+def test_decode_layer_fused(dev, R):
+    """router + experts in the four launches of hmoe_moe_decode_layer; bf16 out = rounded fp32 sum"""
+    log(f"fused decode R={R}")
+    lay = gpu_layer("c0", dev, layer=0)
+    hl = HostLayer(0)
+    x = synth.gen_x(50 + R, R, dev)
+    xn = u16(x)
+    y = torch.zeros((R, H), dtype=torch.float32, device=dev)
+    out = lay.decode(x, y=y)
+    torch.cuda.synchronize()
+    sel_ref, rw_ref = hl.route(xn)
+    assert np.array_equal(lay.sel[:R].cpu().numpy(), sel_ref)
+    assert np.array_equal(u16(lay.rw[:R]), rw_ref)
+    yh = y.cpu().numpy()
+    ma, mr = parity(yh, hl.moe(xn, sel_ref, rw_ref))
+    log(f"  max|d| {ma:.3e} mean-rel {mr:.3e}")
+    assert ma <= MAX_ABS and mr <= MEAN_REL
+    assert np.array_equal(u16(out), O.f32_to_bf16(yh))
+
+
+def test_stack_layers_and_graph(dev):
+    """two layers with residual + RMSNorm between them: norm bit-exact, routing bit-exact, each layer's output within
+    tolerance (checked on the GPU's own layer inputs); the captured hipGraph replays bit-identically"""
+    log("stack of 2 layers, R=4")
+    _LAYERS.clear()
+    torch.cuda.empty_cache()
+    R = 4
+    layers = [synth.make_layer(l, dev) for l in range(2)]
+    ws = [synth.gen_normal(synth.key(synth.SEED, l, synth.KIND["NORM_W"]), H, dev, 1.0, 0.02) for l in range(2)]
+    st = DecodeStack(layers, ws, R)
+    x = synth.gen_x(4, R, dev)
+    st.x.copy_(x)
+    tr = []
+    h_eager = st.step(trace=tr).clone()
+    torch.cuda.synchronize()
+    h_prev = x.float().cpu().numpy()
+    y_prev = None
+    for l, (r_after, xn, y, sel, rw) in enumerate(tr):
+        hl = HostLayer(l)
+        r_ref, xn_ref = O.residual_rmsnorm(h_prev, y_prev, ws[l].cpu().numpy(), 1e-5)
+        assert np.array_equal(r_after.cpu().numpy().view(np.uint32), r_ref.view(np.uint32))
+        assert np.array_equal(u16(xn), xn_ref)
+        sel_ref, rw_ref = hl.route(xn_ref)
+        assert np.array_equal(sel.cpu().numpy(), sel_ref) and np.array_equal(u16(rw), rw_ref)
+        ma, mr = parity(y.cpu().numpy(), hl.moe(xn_ref, sel_ref, rw_ref))
+        log(f"  layer {l}: max|d| {ma:.3e} mean-rel {mr:.3e}")
+        assert ma <= MAX_ABS and mr <= MEAN_REL
+        h_prev, y_prev = r_after.cpu().numpy(), y.cpu().numpy()
+    assert np.array_equal(h_eager.cpu().numpy(), (tr[-1][0] + tr[-1][2]).cpu().numpy())
+    st.capture()
+    for rep in range(3):
+        st.x.copy_(x)
+        st.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(st.h, h_eager), f"replay {rep} differs from the eager step"
+        junk = torch.randn(1 << 20, device=dev).sum()           # eager work between replays
+        torch.cuda.synchronize()
+    del st, layers
+    torch.cuda.empty_cache()
 
 
 # ---- prefill -----------------------------------------------------------------------------------------------------
