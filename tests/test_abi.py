@@ -1,0 +1,98 @@
+"""CPU tests of the product's host side: the C ABI loads and exports every declared symbol (no GPU call), the host
+packers of the gfx950 layouts, the ingest of the reference's moe4 weights, the key derivation and the Zipf bias."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import pyoracle as O
+from hecate_amd import _lib, synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    src = open(os.path.join(ROOT, "include", "hecate_moe.h")).read()
+    return sorted(set(re.findall(r"^(?:int|size_t|const char\*)\s+(hmoe_\w+)\(", src, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    syms = declared_symbols()
+    assert len(syms) >= 20
+    missing = [s for s in syms if not hasattr(L, s)]
+    assert not missing, missing
+    assert set(syms) == set(_lib.SIGNATURES), "ctypes signatures and header disagree"
+    assert _lib.lib().hmoe_version() == 1
+
+
+def test_error_path_sets_message():
+    L = _lib.lib()
+    rc = L.hmoe_pack_i4(None, None, 16, 128, None, None)
+    assert rc == 1 and b"null" in L.hmoe_last_error()
+    with pytest.raises(RuntimeError, match="shape"):
+        buf = np.zeros(64, np.uint8)
+        _lib.call("hmoe_pack_i4", buf.ctypes.data, buf.ctypes.data, 15, 128, buf.ctypes.data, buf.ctypes.data)
+
+
+@pytest.mark.parametrize("N,K", [(16, 128), (64, 384), (2048, 6144)])
+def test_pack_unpack_round_trip_and_layout(N, K):
+    rng = np.random.default_rng(N)
+    codes = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    scales = rng.integers(0, 65536, (N, K // 128), dtype=np.uint16)
+    q = np.empty(N * K // 2, np.uint8); s = np.empty(N * K // 128, np.uint16)
+    _lib.call("hmoe_pack_i4", codes.ctypes.data, scales.ctypes.data, N, K, q.ctypes.data, s.ctypes.data)
+    c2 = np.empty_like(codes); s2 = np.empty_like(scales)
+    _lib.call("hmoe_unpack_i4", q.ctypes.data, s.ctypes.data, N, K, c2.ctypes.data, s2.ctypes.data)
+    assert np.array_equal(c2, codes) and np.array_equal(s2, scales)
+    # layout: lane l of tile (nb, kg), dword j, element e holds (row nb*16 + l%16, k = kg*128 + 32j + 8(l/16) + e)
+    # at bit 4(e/2) + 16(e%2); scales [nb][kg][16]
+    w = q.view(np.uint32).reshape(N // 16, K // 128, 64, 4)
+    full = np.stack([codes & 15, codes >> 4], -1).reshape(N, K)
+    for nb, kg, l, j, e in [(0, 0, 0, 0, 0), (0, 0, 17, 2, 5), (N // 16 - 1, K // 128 - 1, 63, 3, 7), (0, 0, 35, 1, 1)]:
+        row, k = nb * 16 + l % 16, kg * 128 + 32 * j + 8 * (l // 16) + e
+        assert (w[nb, kg, l, j] >> (4 * (e // 2) + 16 * (e % 2))) & 15 == full[row, k]
+    assert s.reshape(N // 16, K // 128, 16)[0, 0, 5] == scales[5, 0]
+
+
+def test_pack_dense_is_f16_tiles():
+    rng = np.random.default_rng(2)
+    N, K = 32, 64
+    w = O.f32_to_bf16((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    out = np.empty(N * K, np.uint16)
+    _lib.call("hmoe_pack_dense", w.ctypes.data, N, K, out.ctypes.data)
+    t = out.reshape(N // 16, K // 32, 64, 8)
+    f16 = O.bf16_to_f32(w).astype(np.float16).view(np.uint16)
+    for nb, ks, l, e in [(0, 0, 0, 0), (1, 1, 63, 7), (0, 1, 20, 3)]:
+        assert t[nb, ks, l, e] == f16[nb * 16 + l % 16, ks * 32 + 8 * (l // 16) + e]
+
+
+def test_repack_reference_moe4_weights():
+    """tools/quant/gptq_int4.py:74-77 pack_u4 (the reference's fragment order, restated as a permutation of the
+    code tensor) + fp32 row scales -> this build's I4G128: same codes, scale = bf16(row scale) in every group"""
+    rng = np.random.default_rng(3)
+    N, K = 128, 256
+    codes = rng.integers(0, 16, (N, K), dtype=np.uint8)
+    c = codes.reshape(N // 64, 4, 2, 8, K // 64, 4, 2, 4, 2).transpose(0, 4, 1, 3, 7, 5, 8, 6, 2).reshape(-1, 2)
+    frag = (c[:, 0] | (c[:, 1] << 4)).astype(np.uint8)
+    rs = (rng.random(N) * 0.01).astype(np.float32)
+    q = np.empty(N * K // 2, np.uint8); s = np.empty(N * K // 128, np.uint16)
+    _lib.call("hmoe_repack_moe4", frag.ctypes.data, rs.ctypes.data, N, K, q.ctypes.data, s.ctypes.data)
+    c2 = np.empty((N, K // 2), np.uint8); s2 = np.empty((N, K // 128), np.uint16)
+    _lib.call("hmoe_unpack_i4", q.ctypes.data, s.ctypes.data, N, K, c2.ctypes.data, s2.ctypes.data)
+    assert np.array_equal(np.stack([c2 & 15, c2 >> 4], -1).reshape(N, K), codes)
+    assert np.array_equal(s2, np.repeat(O.f32_to_bf16(rs)[:, None], K // 128, 1))
+
+
+def test_key_derivation_matches_the_shared_header():
+    for args in [(0, 0, 0, 0), (synth.SEED, 3, 5, 255), (2 ** 63 + 5, 15, 14, 1)]:
+        assert synth.key(*args) == O.key(*args)
+
+
+def test_zipf_tau_is_the_calibrated_one():
+    assert abs(synth.calibrate_zipf_tau(rows=8000) - synth.ZIPF_TAU) < 0.003
+    b = synth.zipf_bias()
+    order = synth.popularity_order()
+    assert np.all(np.diff(b[np.array(order)]) < 0) and sorted(order) == list(range(256))

@@ -1,0 +1,341 @@
+"""Pins the CPU oracle (oracle/hmoe_oracle.c) with checks that do not restate its code:
+
+  conversions      torch / numpy RNE conversions, exhaustive over f16
+  generator        series functions vs numpy within ulps; normal moments / quantiles; code layout vs a pure-Python
+                   restatement of the counter hash; code histogram
+  router logits    fp64 matmul error bound; the fixed chain / segment order emulated exactly with Fractions
+  router select    numpy lexsort top-k on (-key, index); bias = 0 reduces to top-k of the logits; forced ties
+  dispatch         numpy stable argsort + bincount (tier_split.py:405-412 itself); inverse map
+  pick_groups      brute-force block enumeration; hecate_amd.tier.pick_groups; invariants
+  expert layer     numpy fp64 GEMVs on dequantised weights (tiny shapes); q8_0 mode: a many-pick job equals the sum
+                   of its one-pick jobs bit for bit (tools/dev/test_grace_picks.py:63-80) and stays near the exact mode
+  rmsnorm          fp64 within one bf16 ulp; the fixed fp32 order emulated exactly with Fractions
+Nothing is unpinned: every oracle function used by the GPU parity tests has at least one of these checks.
+"""
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as O
+from hecate_amd import synth, tier
+
+
+# ---- conversions --------------------------------------------------------------------------------------------------
+
+def test_f16_exhaustive_and_rne():
+    h = np.arange(65536, dtype=np.uint16)
+    f = O.f16_to_f32(h)
+    ref = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(f[~nan].view(np.uint32), ref[~nan].view(np.uint32)) and np.isnan(f[nan]).all()
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(200000).astype(np.float32) * s for s in (1e-7, 1e-5, 1e-3, 1.0, 3e4)])
+    # exact ties and the subnormal / overflow edges
+    x = np.concatenate([x, (np.arange(-2048, 2048) + 0.5).astype(np.float32) * np.float32(2 ** -24),
+                        np.array([65504, 65519.99, 65520, 1e6, -1e6, 2 ** -25, 2 ** -24, 6.1e-5], np.float32)])
+    assert np.array_equal(O.f32_to_f16(x), x.astype(np.float16).view(np.uint16))
+
+
+def test_bf16_rne_matches_torch():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.standard_normal(300000).astype(np.float32) * s for s in (1e-30, 1e-3, 1.0, 1e30)])
+    x = np.concatenate([x, (np.arange(1, 4000, dtype=np.uint32) * 0x8000 + 0x3f800000).view(np.float32)])
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.f32_to_bf16(x), ref)
+
+
+# ---- generator ----------------------------------------------------------------------------------------------------
+
+def test_exp_series_within_ulps():
+    xs = np.linspace(-80, 80, 20001, dtype=np.float32)
+    got = np.array([O.expf(v) for v in xs[::7]], np.float64)
+    ref = np.exp(xs[::7].astype(np.float64))
+    assert np.max(np.abs(got - ref) / ref) < 4e-7
+
+
+def test_normals_moments_and_quantiles():
+    from scipy.stats import norm
+    z = O.normal_f32(synth.key(1, 2, 3), 2_000_000)
+    assert abs(z.mean()) < 3e-3 and abs(z.std() - 1) < 3e-3
+    q = np.quantile(z, [0.001, 0.01, 0.1, 0.5, 0.9, 0.99, 0.999])
+    assert np.allclose(q, norm.ppf([0.001, 0.01, 0.1, 0.5, 0.9, 0.99, 0.999]), atol=0.02)
+    b = O.normal_bf16(synth.key(1, 2, 3), 1000, 0.02)
+    assert np.array_equal(b, O.f32_to_bf16((0.02 * z[:1000]).astype(np.float32)))
+
+
+def test_codes_layout_and_histogram():
+    N, K = 32, 256
+    k = synth.key(9, 1, synth.KIND["GATE_Q"], 7)
+    c = O.codes(k, N, K)
+    for n, kk in [(0, 0), (0, 1), (0, 15), (0, 16), (3, 77), (31, 255), (17, 128)]:
+        flat = n * K + kk
+        code = (synth.bits(k, flat >> 4) >> (4 * (flat & 15))) & 15
+        byte = c[n, kk // 2]
+        assert code == ((byte >> 4) if kk & 1 else (byte & 15))
+    big = O.codes(k, 2048, 6144)
+    hist = np.bincount(np.concatenate([big.ravel() & 15, big.ravel() >> 4]), minlength=16)
+    assert np.all(np.abs(hist / hist.mean() - 1) < 0.01)
+
+
+def test_scales_are_abs_normal_bf16():
+    s = O.scales(synth.key(2, 0, 6, 1), 2048, 6144, 0.004)
+    f = O.bf16_to_f32(s)
+    assert (f >= 0).all() and abs(f.mean() - 0.004 * np.sqrt(2 / np.pi)) < 1e-4
+
+
+# ---- router -------------------------------------------------------------------------------------------------------
+
+def _fma32(a, b, c):
+    """exact single-rounding fmaf through Fractions"""
+    return np.float32(float(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))))
+
+
+def test_router_logits_bound_and_exact_order():
+    rng = np.random.default_rng(3)
+    R, E, K = 3, 256, 6144
+    x = O.f32_to_bf16(rng.standard_normal((R, K)).astype(np.float32))
+    w = (rng.standard_normal((E, K)) * 0.02).astype(np.float32)
+    lg = O.router_logits(x, w)
+    xf = O.bf16_to_f32(x).astype(np.float64)
+    ref = xf @ w.astype(np.float64).T
+    bound = 1.2e-7 * 2 * K * (np.abs(xf) @ np.abs(w.astype(np.float64)).T) ** 1.0 / np.sqrt(K)
+    assert np.all(np.abs(lg - ref) <= bound + 1e-6)
+    # the exact fp32 order on a small case: K = 512 (8 segments of 64 = 2 chunks of 32)
+    Ks = 512
+    xs = O.f32_to_bf16(rng.standard_normal((1, Ks)).astype(np.float32))
+    ws = (rng.standard_normal((2, Ks)) * 0.02).astype(np.float32)
+    got = O.router_logits(xs, ws)
+    xv = O.bf16_to_f32(xs)[0]
+    for e in range(2):
+        t = np.float32(0)
+        for s0 in range(0, Ks, Ks // 8):
+            seg = np.float32(0)
+            for c in range(s0, s0 + Ks // 8, 32):
+                acc = np.float32(0)
+                for k in range(c, c + 32):
+                    acc = _fma32(xv[k], ws[e, k], acc)
+                seg = np.float32(seg + acc)
+            t = np.float32(t + seg)
+        assert np.float32(got[0, e]).view(np.uint32) == t.view(np.uint32)
+
+
+def _select_numpy(lg, bias, topk=8, scale=2.5):
+    a = np.array([[O.expf(-v) for v in row] for row in lg], np.float32)
+    a = (np.float32(1) / (np.float32(1) + a)).astype(np.float32)
+    key = (a + (bias if bias is not None else np.float32(0))).astype(np.float32)
+    sel, rw = [], []
+    for r in range(lg.shape[0]):
+        order = np.lexsort((np.arange(lg.shape[1]), -key[r].astype(np.float64)))[:topk]
+        s = np.float32(0)
+        for e in order:
+            s = np.float32(s + a[r, e])
+        sel.append(order)
+        rw.append([np.float32(np.float32(a[r, e] * np.float32(scale)) / np.float32(s + np.float32(1e-20))) for e in order])
+    return np.array(sel, np.int64), np.array(rw, np.float32).astype(np.float16).view(np.uint16)
+
+
+def test_router_select_matches_lexsort_topk():
+    rng = np.random.default_rng(4)
+    lg = (rng.standard_normal((40, 256)) * 1.57).astype(np.float32)
+    bias = (rng.standard_normal(256) * 0.01).astype(np.float32)
+    sel, rw = O.router_select(lg, bias)
+    s2, r2 = _select_numpy(lg, bias)
+    assert np.array_equal(sel, s2) and np.array_equal(rw, r2)
+    w = O.f16_to_f32(rw).astype(np.float64).sum(1)
+    assert np.all(np.abs(w - 2.5) < 8 * 2.5 * 2 ** -11)
+    assert all(len(set(r)) == 8 for r in sel)
+
+
+def test_router_select_bias_zero_is_topk_of_logits_and_ties_lowest_index():
+    rng = np.random.default_rng(5)
+    lg = (rng.standard_normal((20, 256)) * 1.57).astype(np.float32)
+    sel, _ = O.router_select(lg, None)
+    ref = np.argsort(-lg.astype(np.float64), axis=1, kind="stable")[:, :8]
+    assert np.array_equal(sel, ref)
+    tie = np.zeros((1, 256), np.float32)
+    tie[0, [200, 5, 77, 3]] = 4.0
+    sel, _ = O.router_select(tie, None)
+    assert list(sel[0]) == [3, 5, 77, 200, 0, 1, 2, 4]
+
+
+# ---- dispatch -----------------------------------------------------------------------------------------------------
+
+def test_dispatch_is_stable_argsort_bincount():
+    rng = np.random.default_rng(6)
+    T, n, lo = 500, 64, 16
+    sel = np.stack([rng.choice(n + 40, 8, replace=False) for _ in range(T)]).astype(np.int64)
+    rw = O.f32_to_f16(rng.random((T, 8)).astype(np.float32))
+    counts, tok, eid, wt, inv = O.dispatch(sel, rw, lo, n)
+    fs = sel.ravel() - lo
+    keep = (fs >= 0) & (fs < n)
+    order = np.argsort(np.where(keep, fs, n + 1), kind="stable")[: keep.sum()]
+    assert np.array_equal(counts, np.bincount(fs[keep], minlength=n))
+    assert np.array_equal(tok, order // 8) and np.array_equal(eid, fs[order])
+    assert np.array_equal(wt, O.f16_to_f32(rw.ravel()[order]))
+    assert np.array_equal(inv[order], np.arange(len(order))) and np.all(inv[~keep] == -1)
+
+
+def _pick_groups_brute(counts, bm, balance):
+    rows, pos = [], 0
+    for e, c in enumerate(counts):
+        if c:
+            nb = -(-c // bm)
+            sizes = [c // nb + (1 if k < c % nb else 0) for k in range(nb)] if balance else \
+                [min(bm, c - bm * k) for k in range(nb)]
+            first = pos
+            for s in sizes:
+                rows.append((e, first, s, 0))
+                first += s
+        pos += c
+    return np.array(rows, np.int32).reshape(-1, 4)
+
+
+@pytest.mark.parametrize("bm,balance", [(64, False), (256, True), (16, False), (7, True)])
+def test_pick_groups_brute_force(bm, balance):
+    rng = np.random.default_rng(bm)
+    counts = rng.multinomial(3000, np.ones(100) / 100)
+    counts[[3, 50]] = 0
+    ref = _pick_groups_brute(counts, bm, balance)
+    assert np.array_equal(O.pick_groups(counts, bm, balance), ref)
+    (p0, p1, rbt), = list(tier.pick_groups(counts, counts.sum(), bm, balance))
+    assert (p0, p1) == (0, counts.sum()) and np.array_equal(rbt, ref)
+    assert np.all(ref[:, 2] <= bm) and np.array_equal(np.bincount(ref[:, 0], ref[:, 2], 100).astype(np.int64), counts)
+
+
+def test_pick_groups_splits_at_npos():
+    counts = np.array([30, 0, 50, 20, 64, 1], np.int64)
+    groups = list(tier.pick_groups(counts, 100, 16))
+    assert [(g[0], g[1]) for g in groups] == [(0, 100), (100, 165)]
+    assert groups[1][2][0, 0] == 4 and groups[1][2][0, 1] == 0
+    with pytest.raises(ValueError):
+        list(tier.pick_groups(counts, 40, 16))
+
+
+# ---- expert layer -------------------------------------------------------------------------------------------------
+
+def _tiny_layer(rng, H=256, I=128, E=6):
+    ex = []
+    for e in range(E):
+        d = {}
+        for m, (N, K) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
+            d[m + "_q"] = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+            d[m + "_s"] = O.f32_to_bf16(np.abs(rng.standard_normal((N, K // 128)) * 0.01).astype(np.float32))
+        ex.append(d)
+    sh = (O.f32_to_bf16((rng.standard_normal((I, H)) * 0.05).astype(np.float32)),
+          O.f32_to_bf16((rng.standard_normal((I, H)) * 0.05).astype(np.float32)),
+          O.f32_to_bf16((rng.standard_normal((H, I)) * 0.05).astype(np.float32)))
+    return ex, sh
+
+
+def _moe_numpy(x, sel, rw, ex, sh, H, I, lo=0):
+    xf = O.bf16_to_f32(x).astype(np.float64)
+    silu = lambda g: g / (1 + np.exp(-g))
+    deq = lambda d, m, N, K: O.dequant(d[m + "_q"], d[m + "_s"], N, K).astype(np.float64)
+    out = np.zeros((x.shape[0], H))
+    for r in range(x.shape[0]):
+        for k in range(sel.shape[1]):
+            e = int(sel[r, k]) - lo
+            if 0 <= e < len(ex):
+                w = float(O.f16_to_f32(rw[r, k:k + 1])[0])
+                d = ex[e]
+                a = silu(deq(d, "gate", I, H) @ xf[r]) * (deq(d, "up", I, H) @ xf[r]) * w
+                out[r] += deq(d, "down", H, I) @ a
+        if sh is not None:
+            g = O.bf16_to_f32(sh[0]).astype(np.float64) @ xf[r]
+            u = O.bf16_to_f32(sh[1]).astype(np.float64) @ xf[r]
+            out[r] += O.bf16_to_f32(sh[2]).astype(np.float64) @ (silu(g) * u)
+    return out
+
+
+def test_dequant_closed_form():
+    rng = np.random.default_rng(7)
+    q = rng.integers(0, 256, (16, 128), dtype=np.uint8)
+    s = O.f32_to_bf16(rng.random((16, 2)).astype(np.float32))
+    d = O.dequant(q, s, 16, 256)
+    codes = np.stack([q & 15, q >> 4], -1).reshape(16, 256).astype(np.int32) - 8
+    assert np.array_equal(d, (codes * np.repeat(O.bf16_to_f32(s), 128, 1)).astype(np.float32))
+
+
+def test_moe_exact_matches_numpy_fp64():
+    rng = np.random.default_rng(8)
+    H, I = 256, 128
+    ex, sh = _tiny_layer(rng, H, I)
+    x = O.f32_to_bf16(rng.standard_normal((5, H)).astype(np.float32))
+    sel = np.array([[1, 3, 9, 0, 5, 2, 4, 7]] * 5, np.int64) + 10
+    sel[2] = [15, 11, 10, 13, 12, 14, 30, 40]
+    rw = O.f32_to_f16(rng.random((5, 8)).astype(np.float32))
+    tab = O.ExpertTable(ex)
+    got = O.moe(0, x, sel, rw, tab, 10, len(ex), sh, H=H, I=I, threads=4)
+    ref = _moe_numpy(x, sel, rw, ex, sh, H, I, lo=10)
+    assert np.max(np.abs(got - ref)) <= 1e-6 * np.max(np.abs(ref))
+    part = rng.standard_normal((5, H)).astype(np.float32)
+    got2 = O.moe(0, x, sel, rw, tab, 10, len(ex), None, out=part.copy(), accumulate=True, H=H, I=I, threads=4)
+    ref2 = _moe_numpy(x, sel, rw, ex, None, H, I, lo=10) + part
+    assert np.max(np.abs(got2 - ref2)) <= 1e-6 * np.max(np.abs(ref2))
+
+
+def test_picks_first_appearance_order():
+    sel = np.array([[5, 2, 9, 1], [2, 7, 5, 3]], np.int64)
+    rw = O.f32_to_f16(np.array([[0.5, 0.25, 1, 2], [0.125, 1, 4, 1]], np.float32))
+    pick, wgt = O.picks(sel, rw, 1, 8)
+    assert list(pick) == [4, 1, 0, 6, 2]
+    assert np.allclose(wgt[0], [0.5, 4]) and np.allclose(wgt[1], [0.25, 0.125]) and np.allclose(wgt[3], [0, 1])
+
+
+def test_q8_many_picks_equal_sum_of_one_pick_jobs():
+    """tools/dev/test_grace_picks.py:63-80: a job's partial is each row's fp32 sum, from 0, of its picks' outputs in
+    pick order; a one-pick job's partial is exactly that pick's output"""
+    rng = np.random.default_rng(9)
+    H, I = 256, 128
+    ex, _ = _tiny_layer(rng, H, I, E=6)
+    tab = O.ExpertTable(ex)
+    for trial in range(6):
+        R = int(rng.integers(1, 9))
+        sel = np.stack([rng.choice(40, 8, replace=False) for _ in range(R)]).astype(np.int64)
+        rw = O.f32_to_f16((rng.random((R, 8)) * 0.4 + 0.01).astype(np.float32))
+        x = O.f32_to_bf16((rng.standard_normal((R, H)) * rng.choice([0.3, 1.0, 4.0])).astype(np.float32))
+        got = O.moe(1, x, sel, rw, tab, 0, 6, None, H=H, I=I, threads=2)
+        pick, _ = O.picks(sel, rw, 0, 6)
+        ref = np.zeros((R, H), np.float32)
+        for e in pick:
+            s1 = np.full_like(sel, 39); r1 = np.zeros_like(rw)
+            for r in range(R):
+                hit = np.where(sel[r] == e)[0]
+                if len(hit):
+                    s1[r, 0] = e; r1[r, 0] = rw[r, hit[0]]
+            ref = (ref + O.moe(1, x, s1, r1, tab, 0, 6, None, H=H, I=I, threads=2)).astype(np.float32)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+        ex_ = O.moe(0, x, sel, rw, tab, 0, 6, None, H=H, I=I, threads=2)
+        assert np.abs(got - ex_).mean() / np.abs(ex_).mean() < 0.03
+
+
+# ---- rmsnorm ------------------------------------------------------------------------------------------------------
+
+def test_rmsnorm_fp64_and_exact_order():
+    rng = np.random.default_rng(10)
+    H = 512
+    r = rng.standard_normal((2, H)).astype(np.float32)
+    a = rng.standard_normal((2, H)).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(H)).astype(np.float32)
+    r2, xn = O.residual_rmsnorm(r, a, w, 1e-5)
+    assert np.array_equal(r2, (r + a).astype(np.float32))
+    v = (r + a).astype(np.float64)
+    ref = v / np.sqrt((v ** 2).mean(1, keepdims=True) + 1e-5) * w
+    assert np.all(np.abs(O.bf16_to_f32(xn) - ref) <= np.abs(ref) * 2 ** -8 + 1e-7)
+    vf = (r + a).astype(np.float32)[0]
+    part = []
+    for t in range(256):
+        p = np.float32(0)
+        for k in range(t, H, 256):
+            p = _fma32(vf[k], vf[k], p)
+        part.append(p)
+    off = 128
+    while off:
+        for t in range(off):
+            part[t] = np.float32(part[t] + part[t + off])
+        off >>= 1
+    rmf = np.float32(np.float32(1) / np.sqrt(np.float32(part[0] / np.float32(H)) + np.float32(1e-5), dtype=np.float32))
+    exp = O.f32_to_bf16(((vf * rmf).astype(np.float32) * w).astype(np.float32))
+    assert np.array_equal(xn[0], exp)
