@@ -187,6 +187,19 @@ def graph_workload(torch, synth, steps, warmup, dev, n_layers=16, R=4):
     return res
 
 
+def copy_workload(torch, steps, warmup, dev, nbytes=1 << 30):
+    """torch's device copy of a known size: the calibration of the FETCH_SIZE / WRITE_SIZE counters (KiB per
+    dispatch) and the measured copy bandwidth of the box"""
+    src = torch.empty(nbytes // 4, dtype=torch.int32, device=dev).fill_(7)
+    dst = torch.empty_like(src)
+    el = timed(torch, lambda i: dst.copy_(src), steps, warmup)
+    res = {"bytes_read": nbytes, "bytes_written": nbytes, "us_per_copy": el / steps * 1e6,
+           "gbs_read_plus_write": 2 * nbytes / (el / steps) / 1e9}
+    del src, dst
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(budget_s=12.0):
     """the CPU expert path (oracle q8_0 mode: runtime/tier/cpuband.cpp restated) on the 16-row Zipf step of layer 0,
     as two 8-row jobs (cpuband caps a job at 8 rows) after the CPU router, timed on this host's cores"""
@@ -240,7 +253,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None, choices=[None, "decode16", "decode1", "decode8", "prefill", "partial",
-                                                     "graph16"])
+                                                     "graph16", "copy"])
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the path would shard by "
@@ -271,6 +284,8 @@ def main():
     if only in (None, "graph16"):
         extra["graph_16_layers_b4"] = graph_workload(torch, synth, max(20, K // 4), max(3, W // 4), dev)
         log(f"[bench] graph16: {json.dumps(extra['graph_16_layers_b4'])}")
+    if only == "copy":
+        extra["copy_1gib"] = copy_workload(torch, max(10, K // 10), 3, dev)
     if head is None:
         print(json.dumps({"extra": extra}))
         return
