@@ -68,7 +68,7 @@ __global__ void gen_i4_kernel(uint64_t key_q, uint64_t key_s, float sigma_s, int
         if (l < 16)
         {
             const int r = nb * 16 + l;
-            s[tile * 16 + l] = hmoe_f2bf(fabsf(sigma_s * hmoe_normal(key_s, (uint64_t) r * KG + kg)));
+            s[(size_t) r * KG + kg] = hmoe_f2bf(fabsf(sigma_s * hmoe_normal(key_s, (uint64_t) r * KG + kg)));
         }
     }
 }
@@ -117,7 +117,7 @@ __global__ void dequant_kernel(const u32x4* __restrict__ q, const uint16_t* __re
         const size_t tile = i >> 6;
         const int kg = (int) (tile % KG), nb = (int) (tile / KG);
         const int row = nb * 16 + (l & 15);
-        const float sc = bf2f(s[tile * 16 + (l & 15)]);
+        const float sc = bf2f(s[(size_t) row * KG + kg]);
         const u32x4 v = q[i];
         #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -222,8 +222,8 @@ extern "C" int hmoe_pack_i4(const uint8_t* codes, const uint16_t* scales, int N,
                     for (int e = 0; e < 8; ++e) word |= canon_code(codes, K, row, k0 + e) << nib_shift(e);
                     q[(tile * 64 + l) * 4 + j] = word;
                 }
-            for (int r = 0; r < 16; ++r) s[tile * 16 + r] = scales[(size_t) (nb * 16 + r) * KG + kg];
         }
+    memcpy(s, scales, sizeof(uint16_t) * (size_t) N * KG);       // scales keep the canonical row-major layout
     return HMOE_OK;
 }
 
@@ -251,8 +251,8 @@ extern "C" int hmoe_unpack_i4(const void* q_host, const void* s_host, int N, int
                         codes[(size_t) row * (K / 2) + k / 2] |= (uint8_t) ((k & 1) ? (c << 4) : c);
                     }
                 }
-            for (int r = 0; r < 16; ++r) scales[(size_t) (nb * 16 + r) * KG + kg] = s[tile * 16 + r];
         }
+    memcpy(scales, s, sizeof(uint16_t) * (size_t) N * KG);
     return HMOE_OK;
 }
 

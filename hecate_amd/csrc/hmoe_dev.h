@@ -25,19 +25,31 @@ int hip_check(hipError_t e, const char* what);
 #define HMOE_REQUIRE(cond, ...) do { if (!(cond)) return ::hmoe::set_error(HMOE_ERR_ARG, __VA_ARGS__); } while (0)
 #define HMOE_LAUNCHED(what) ::hmoe::hip_check(hipGetLastError(), what)
 
+// ---- compile-time loop: f(ic<0>{}), ..., f(ic<N-1>{}) (register arrays indexed by a constant stay in registers) ----
+template <int V> struct ic { static constexpr int value = V; };
+template <int N, int K = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f)
+{
+    if constexpr (K < N) { f(ic<K>{}); static_for<N, K + 1>(f); }
+}
+
 // ---- conversions ----
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t) b << 16); }
 
 // 8 codes of one I4G128 dword -> 8 exact f16 values q = code - 8, element e of the MFMA operand at nibble bit
 // 4(e/2) + 16(e%2): (code | 0x6400) is the f16 1024 + code (0x6400 = 1024, one unit per mantissa step), minus 1032;
 // the odd nibble of each byte lands 4 bits up, 1024 + 16 code, scaled by 1/16 and offset by -72 (all exact).
+// The masks and the exponent sit in registers the compiler cannot fold into literals, so each (w & mask) | 0x6400..
+// is one v_and_or_b32 (a VOP3 of gfx9 takes no 32-bit literal, and two literals would cost two instructions).
 __device__ __forceinline__ f16x8 dq8(uint32_t w)
 {
+    uint32_t m0 = 0x000f000fu, m1 = 0x00f000f0u, mg = 0x64006400u;
+    asm volatile("" : "+v"(m0), "+v"(m1), "+v"(mg));
     const uint32_t top = w >> 8;
-    const uint32_t h0 = (w & 0x000f000fu) | 0x64006400u;
-    const uint32_t h1 = (w & 0x00f000f0u) | 0x64006400u;
-    const uint32_t h2 = (top & 0x000f000fu) | 0x64006400u;
-    const uint32_t h3 = (top & 0x00f000f0u) | 0x64006400u;
+    const uint32_t h0 = (w & m0) | mg;
+    const uint32_t h1 = (w & m1) | mg;
+    const uint32_t h2 = (top & m0) | mg;
+    const uint32_t h3 = (top & m1) | mg;
     const f16x2 m1032 = {(_Float16) -1032.0f, (_Float16) -1032.0f};
     const f16x2 s16 = {(_Float16) 0.0625f, (_Float16) 0.0625f};
     const f16x2 m72 = {(_Float16) -72.0f, (_Float16) -72.0f};
@@ -60,9 +72,15 @@ __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c)
 
 __device__ __forceinline__ f16x8 as_f16x8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
 
-// global loads of weights that are read once (nontemporal: do not keep them in the caches)
-__device__ __forceinline__ u32x4 ldw16(const void* p) { return __builtin_nontemporal_load((const u32x4*) p); }
-__device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*) p; }
+// Loads from global memory through pointers the compiler cannot trace to a kernel argument (expert addresses read from
+// a table): the explicit global address space makes them global_load. A generic pointer would give flat_load, which
+// also counts against the LDS wait counter, so every LDS wait would drain the weight loads in flight.
+#define HMOE_GLOBAL __attribute__((address_space(1)))
+template <typename T> __device__ __forceinline__ T ldg(const void* p) { return *(const HMOE_GLOBAL T*) p; }
+// weights read once: nontemporal (not kept in the caches)
+__device__ __forceinline__ u32x4 ldw16(const void* p) { return __builtin_nontemporal_load((const HMOE_GLOBAL u32x4*) p); }
+__device__ __forceinline__ u32x4 ld16(const void* p) { return ldg<u32x4>(p); }
+__device__ __forceinline__ u32x2 ld8(const void* p) { return ldg<u32x2>(p); }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 

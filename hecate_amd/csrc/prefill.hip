@@ -149,7 +149,7 @@ __device__ __forceinline__ void a_i4(const uint8_t* q, const uint8_t* s, int nb,
 {
     const int l = threadIdx.x & 63;
     const u32x4 w = ldw16(q + ((size_t) (nb * KG + kg) * 64 + l) * 16);
-    const uint16_t sb = *(const uint16_t*) (s + ((size_t) (nb * KG + kg) * 16 + (l & 15)) * 2);
+    const uint16_t sb = ldg<uint16_t>(s + ((size_t) (nb * 16 + (l & 15)) * KG + kg) * 2);
     const _Float16 sh = (_Float16) bf2f(sb);
     const f16x8 s8 = {sh, sh, sh, sh, sh, sh, sh, sh};
     #pragma unroll

@@ -17,7 +17,7 @@ def _req(cond, msg):
 
 
 def scratch(device):
-    """moe4.cu:897-902: [act, gu32, ctr_a, y32, ctr_b], zeroed (the kernels leave them zeroed)"""
+    """moe4.cu:897-902: [act, gu32, ctr_a, y32, ctr_b] (workspace: any contents work, gu32 / ctr_b are unused)"""
     dev = torch.device(device)
     L = lib()
     nb = [int(L.hmoe_moe4_scratch_bytes(i)) for i in range(5)]

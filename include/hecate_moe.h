@@ -7,14 +7,16 @@
  *     (runtime/tier/tier_split.py:206-214, 246); the caller owns every buffer, the library never frees;
  *   - work is queued on `stream` (a hipStream_t; NULL = default stream), asynchronously, with a static launch shape
  *     and no allocation, host synchronisation or hipMemset, so the launches are hipGraph-capturable;
- *   - scratch buffers come back zeroed (self-cleaning) and calls that share one scratch must not overlap;
+ *   - scratch buffers are workspace: no launch reads scratch it has not written in the same call, so any contents
+ *     work (nothing needs zeroing) and calls that share one scratch must not overlap;
  *   - every entry point returns HMOE_OK or an error code; hmoe_last_error() gives the thread's last message.
  *
  * Formats (this build's gfx950 layouts, hmoe_pack_* produce them from the canonical row-major ones):
  *   I4G128 int4 matrix [N][K] (N % 16 == 0, K % 128 == 0): codes in 1 KB tiles of 16 rows x 128 k, tile (nb, kg) at
  *          byte (nb * K/128 + kg) * 1024; lane l (0..63) of a tile holds 16 bytes = 4 dwords, dword j packs the 8 codes
  *          (q + 8) of row nb*16 + l%16 at k = kg*128 + 32j + 8(l/16) + e, e = 0..7, code e at bit 4(e/2) + 16(e%2).
- *          Scales bf16 [N/16][K/128][16]: the 16 row scales of tile (nb, kg), contiguous.
+ *          Scales bf16 [N][K/128], row-major (the canonical layout: a lane that owns row n reads the group scales of
+ *          several k groups with one load).
  *   F16T   dense matrix [N][K] (K % 32 == 0) as f16 in 1 KB tiles of 16 rows x 32 k, tile (nb, ks) at byte
  *          (nb * K/32 + ks) * 1024, lane l holds the 8 f16 of row nb*16 + l%16 at k = ks*32 + 8(l/16) + e.
  *   x      bf16 [R][H] (the MoE input); xh its f16 copy (exact for the reference's fp16 activation range).
@@ -78,8 +80,9 @@ int hmoe_router_fused(const void* x, const float* wt, const float* bias, float* 
  * picks with sel - lo in [0, n_hot) run, tables indexed by sel - lo hold I4G128 codes (gate/up [I][H], down [H][I])
  * and their scales; y fp32 [R][H] is accumulated into. sh_gw / sh_uw / sh_dw: the shared expert as F16T (gate/up
  * [I][H], down [H][I]) or NULL; sh_gs / sh_us / sh_ds must be NULL (the reference's int8 row scales; F16T has none).
- * Scratch (act, gu32, ctr_a, y32, ctr_b) from hmoe_moe4_scratch_bytes (ctr_b unused). blocks: grid size of the
- * gate/up and down kernels (0 = 2 per CU), blocks_a: unused (kept for the reference's argument position).
+ * Scratch (act, gu32, ctr_a, y32, ctr_b) from hmoe_moe4_scratch_bytes (gu32 and ctr_b unused, kept for the argument
+ * positions). blocks: grid size of the routed gate/up and down kernels (0 = one workgroup per CU), blocks_a: unused.
+ * The shared expert runs on a per-device side stream forked from and joined back into `stream` (graph-capturable).
  * R in [1, 16]. */
 size_t hmoe_moe4_scratch_bytes(int which);      /* which: 0 act, 1 gu32, 2 ctr_a, 3 y32, 4 ctr_b */
 int hmoe_moe4_forward(const void* x, const int64_t* sel, const uint16_t* rw, int R, int n_hot,
@@ -89,7 +92,7 @@ int hmoe_moe4_forward(const void* x, const int64_t* sel, const uint16_t* rw, int
                       int lo, const void* sh_gw, const void* sh_uw, const void* sh_dw, const void* sh_gs,
                       const void* sh_us, const void* sh_ds, int xf, void* stream);
 /* the two phases of hmoe_moe4_forward, for callers that time or schedule them apart (this build's addition):
- * gate_up writes act (and the f16 copy of x when xf = 0), down adds into y (ctr_b carries its part count); same
+ * gate_up writes act, down adds into y (ctr_b carries its part count); same
  * arguments and rules as forward */
 int hmoe_moe4_gate_up(const void* x, const int64_t* sel, const uint16_t* rw, int R, int n_hot,
                       const int64_t* gate_w, const int64_t* up_w, const int64_t* gate_s, const int64_t* up_s,
