@@ -37,7 +37,7 @@ SIGNATURES = {
     "hmoe_dispatch": (i32, [P, P, i32, i32, i32, i32, i32, i32, P, P, P, P, P, P, i32, P, P, P]),
     "hmoe_moe4p_scratch_bytes": (sz, [i32, i32, i32]),
     "hmoe_moe4p_forward": (i32, [P, P, P, P, P, i32, i32, i32, P, P, P, P, P, P, P, P, P, P, i32, P, P, i32, i32,
-                                 P, P, P, P]),
+                                 P, P, P, i32, P]),
     "hmoe_residual_rmsnorm": (i32, [P, P, P, i32, f32, P, P, P]),
 }
 

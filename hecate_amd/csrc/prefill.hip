@@ -3,20 +3,15 @@
 //
 // Dispatch: picks sorted by (expert, flat index) by a counting sort with per-block histograms and in-block ranks, so
 // the order equals a stable argsort of the selection; row blocks {expert, first pick, picks, 0} of at most bm picks.
-// GEMMs: workgroup = (row block of <= 64 picks of one expert, 128 output columns). The picks' input rows are gathered,
-// converted to f16 and staged per 128-k group in LDS (double buffered); each of the 4 waves owns 32 output rows of
-// gate and of up (2 strips of 16 each) and decodes its I4G128 tiles straight from HBM into registers (one 16-byte
-// load per lane per tile, exact f16 codes times the f16 group scale), then runs the 16x16x32 MFMA against every
-// 16-pick tile of the block. gu fuses act = silu(g) * u * w (f16), down writes d = W_d act (fp32), fin adds each
+// GEMMs: workgroup = (row block of <= 128 picks of one expert, 128 gate/up or 256 down output columns); see
+// pgemm_kernel. gu fuses act = silu(g) * u * w (f16), down writes d = W_d act (fp32), fin adds each
 // token's picks into out in top-k order (or with atomics, as p4_fin_kernel, when no inverse map is given).
 #include "hmoe_dev.h"
 
 namespace hmoe {
 
-constexpr int PB = 64;                      // picks per row block
-constexpr int PN = 128;                     // output columns per workgroup
+constexpr int PB = 128;                     // picks per row block (dispatch bm <= 128)
 constexpr int PT = 256;                     // threads
-constexpr int XSTR = 128 + 8;               // LDS row stride (f16) of the staged inputs
 constexpr int DBLK = 256;                   // picks per dispatch block
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -107,209 +102,217 @@ __device__ __forceinline__ bool get_block(const int* rbt, int nrb, const int* me
     return b.e >= 0 && b.e < n_tab && b.rows > 0;
 }
 
-// stage one 128-k group of the block's input rows (bf16 rows of x, gathered) into LDS as f16: thread t copies
-// row t/4, 32 values at (t%4)*32
-__device__ __forceinline__ void load_x_bf16(const uint16_t* src_row, int k0, u32x4* v)
+// A pipelined grouped GEMM for both projections. Workgroup = (row block of <= 128 picks of one expert, 64 NS output
+// columns); wave w owns output strips nb0 = 4 NS blockIdx.y + NS w .. + NS (16 rows each) of NMAT matrices (gate and
+// up: NS = 2, or down: NS = 4), so every wave holds 4 weight fragments per k step and reads each 16-pick input
+// fragment from LDS once for 4 MFMAs. Per 128-k group kg:
+//   * the block's input rows are staged in LDS as f16 (double-buffered, one barrier per group); the next group's
+//     rows are loaded into registers while this group computes;
+//   * the weight tiles come from a ring of D groups of unconditional 16-byte loads (and the lane's row scale), issued
+//     D groups ahead, so HBM latency hides behind D groups of MFMA work; each tile is loaded once per workgroup;
+//   * each k step dequantises the 4 weight fragments (exact f16 codes times the f16 group scale) and runs the
+//     16x16x32 MFMA against the block's 16-pick tiles (up to 8).
+// DENSE: the shared expert (F16T, every token, block b = tokens [128 b, 128 b + 128), weight 1); its groups are
+// 4 tiles each.
+template <bool DENSE, int NMAT, int NS>
+struct PFetch
 {
-    #pragma unroll
-    for (int q = 0; q < 4; ++q) v[q] = src_row ? *(const u32x4*) (src_row + k0 + 8 * q) : (u32x4) {0u, 0u, 0u, 0u};
-}
-__device__ __forceinline__ void store_x_bf16(_Float16* xs, const u32x4* v)
+    u32x4 q[NS][NMAT][DENSE ? 4 : 1];
+    uint16_t s[NS][NMAT];
+};
+
+template <bool DENSE, int NMAT, int NS, int D>
+__global__ void __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(2))) pgemm_kernel(
+    const _Float16* __restrict__ xin, const int* __restrict__ tok, const float* __restrict__ wt,
+    const int* __restrict__ rbt, int nrb, const int* __restrict__ meta, int n_tab,
+    const int64_t* __restrict__ w0, const int64_t* __restrict__ w1, const int64_t* __restrict__ s0,
+    const int64_t* __restrict__ s1, const uint8_t* __restrict__ dense0, const uint8_t* __restrict__ dense1,
+    _Float16* __restrict__ ar, float* __restrict__ dout, int T, int off)
 {
-    const int t = threadIdx.x, r = t >> 2, c = (t & 3) * 32;
+    constexpr int K = NMAT == 2 ? H : I;                 // gate/up: x [T][H] -> act; down: act [.][I] -> d
+    constexpr int NOUT = NMAT == 2 ? I : H;
+    constexpr int KG = K / 128, KS = K / 32;
+    static_assert(KG % D == 0, "the ring depth divides the k groups");
+    static_assert(NS * NMAT == 4, "four weight fragments per wave and k step");
+    // the staged input of a 128-k group in MFMA fragment order: 1 KB block (tile tt, k step k) holds lane l's 16 bytes
+    // (pick tt*16 + l%16, k 32k + 8(l/16)) at 16 l, written by one direct global-to-LDS load per block and read back
+    // as one contiguous 1 KB wave read (no bank conflicts); two buffers, the next group loads while one computes
+    __shared__ __attribute__((aligned(16))) u32x4 xs0[32 * 64];
+    __shared__ __attribute__((aligned(16))) u32x4 xs1[32 * 64];
+    Block b;
+    if (DENSE) { b.e = 0; b.p0 = blockIdx.x * PB; b.rows = min(PB, T - b.p0); if (b.rows <= 0) return; }
+    else if (!get_block(rbt, nrb, meta, n_tab, b)) return;
+    const int t = threadIdx.x, w = t >> 6, l = t & 63, row = l & 15;
+    const int nb0 = (blockIdx.y * 4 + w) * NS;
+    const uint8_t* wp[NMAT];
+    const uint8_t* sp[NMAT];
     #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int m = 0; m < NMAT; ++m)
     {
+        wp[m] = DENSE ? (m == 0 ? dense0 : dense1) : (const uint8_t*) (m == 0 ? w0 : w1)[b.e];
+        sp[m] = DENSE ? nullptr : (const uint8_t*) (m == 0 ? s0 : s1)[b.e];
+    }
+    const int ntt = (b.rows + 15) >> 4;
+    // wave w stages tiles 2w and 2w + 1: lane l's source row; a pick past the block re-reads a valid row (its output
+    // columns are never stored), a whole tile past the block reads one fixed 16 bytes
+    const _Float16* src[2];
+    #pragma unroll
+    for (int h = 0; h < 2; ++h)
+    {
+        const int tt = 2 * w + h, pk = tt * 16 + row;
+        const bool in = pk < b.rows, tin = tt < ntt;
+        int srow;
+        if (NMAT == 2)
+        {
+            const int tk = DENSE ? b.p0 + (in ? pk : 0) : tok[b.p0 + (in ? pk : 0)];
+            srow = (unsigned) tk < (unsigned) T ? tk : 0;
+        }
+        else srow = off + b.p0 + (in ? pk : 0);
+        src[h] = xin + (size_t) srow * K + (tin ? 8 * (l >> 4) : 0);
+    }
+    // Direct global-to-LDS loads (16 bytes per lane, lane l at LDS base + 16 l), issued from inline assembly: the
+    // compiler then does not count them, so its own waits for the weight ring stay exact, and the wait that makes a
+    // staged group visible is placed by hand before the barrier (the loads issued after a stage are exactly the
+    // FETCH_LOADS of one ring refill). M0 holds the LDS base of each load; nothing else in this kernel uses M0.
+    constexpr int FETCH_LOADS = DENSE ? NS * NMAT * 4 : NS * NMAT * 2;
+    auto stage = [&](int kg, u32x4* buf) {
+        #pragma unroll
+        for (int h = 0; h < 2; ++h)
+        {
+            const int tt = 2 * w + h;
+            const bool tin = tt < ntt;
+            #pragma unroll
+            for (int k = 0; k < 4; ++k)
+            {
+                const _Float16* gp = src[h] + (tin ? kg * 128 + 32 * k : 0);
+                const uint32_t lds = __builtin_amdgcn_readfirstlane(
+                    (uint32_t) (uintptr_t) (__attribute__((address_space(3))) void*) (buf + (tt * 4 + k) * 64));
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+                asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(gp), "s"(lds) : "memory", "m0");
+#pragma clang diagnostic pop
+            }
+        }
+    };
+    PFetch<DENSE, NMAT, NS> ring[D];
+    auto fetch = [&](int kg, auto sc) {
+        constexpr int s = decltype(sc)::value;
+        #pragma unroll
+        for (int st = 0; st < NS; ++st)
+            #pragma unroll
+            for (int m = 0; m < NMAT; ++m)
+            {
+                const int nb = nb0 + st;
+                if (DENSE)
+                {
+                    #pragma unroll
+                    for (int u = 0; u < 4; ++u) ring[s].q[st][m][u] = ldw16(wp[m] + ((size_t) (nb * KS + kg * 4 + u) * 64 + l) * 16);
+                }
+                else
+                {
+                    ring[s].q[st][m][0] = ldw16(wp[m] + ((size_t) (nb * KG + kg) * 64 + l) * 16);
+                    ring[s].s[st][m] = ldg<uint16_t>(sp[m] + ((size_t) (nb * 16 + row) * KG + kg) * 2);
+                }
+            }
+    };
+    f32x4 acc[NS][NMAT][8];
+    #pragma unroll
+    for (int st = 0; st < NS; ++st)
+        #pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+            #pragma unroll
+            for (int tt = 0; tt < 8; ++tt) acc[st][m][tt] = (f32x4) {0.f, 0.f, 0.f, 0.f};
+    stage(0, xs0);
+    static_for<D>([&](auto sc) {
+        fetch(decltype(sc)::value, sc);
+        __builtin_amdgcn_sched_barrier(0);                  // keep the ring's issue order (waits count in order)
+    });
+    for (int kg0 = 0; kg0 < KG; kg0 += D)
+    {
+        static_for<D>([&](auto sc) {
+            constexpr int s = decltype(sc)::value;
+            const int kg = kg0 + s;
+            const bool even = (kg & 1) == 0;
+            u32x4* cur = even ? xs0 : xs1;
+            // this wave's staged loads of group kg are older than the FETCH_LOADS of the last refill (or, for kg = 0,
+            // than the D prologue refills); the barrier then makes every wave's group kg visible
+            if (kg == 0) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(FETCH_LOADS * D) : "memory");
+            else asm volatile("s_waitcnt vmcnt(%0)" :: "n"(FETCH_LOADS) : "memory");
+            __syncthreads();
+            if (kg + 1 < KG) stage(kg + 1, even ? xs1 : xs0);
+            _Float16 sh[NS][NMAT];
+            #pragma unroll
+            for (int st = 0; st < NS; ++st)
+                #pragma unroll
+                for (int m = 0; m < NMAT; ++m) sh[st][m] = DENSE ? (_Float16) 1.0f : (_Float16) bf2f(ring[s].s[st][m]);
+            #pragma unroll
+            for (int k = 0; k < 4; ++k)
+            {
+                f16x8 a[NS][NMAT];
+                #pragma unroll
+                for (int st = 0; st < NS; ++st)
+                    #pragma unroll
+                    for (int m = 0; m < NMAT; ++m)
+                    {
+                        if (DENSE) a[st][m] = as_f16x8(ring[s].q[st][m][k]);
+                        else
+                        {
+                            const _Float16 h = sh[st][m];
+                            const f16x8 s8 = {h, h, h, h, h, h, h, h};
+                            a[st][m] = dq8(ring[s].q[st][m][0][k]) * s8;
+                        }
+                    }
+                #pragma unroll
+                for (int tt = 0; tt < 8; ++tt)
+                {
+                    if (tt >= ntt) break;
+                    const f16x8 bv = as_f16x8(cur[(tt * 4 + k) * 64 + l]);
+                    #pragma unroll
+                    for (int st = 0; st < NS; ++st)
+                        #pragma unroll
+                        for (int m = 0; m < NMAT; ++m) acc[st][m][tt] = mfma16(a[st][m], bv, acc[st][m][tt]);
+                }
+            }
+            fetch(min(kg + D, KG - 1), sc);                 // refill the slot just used (clamped at the end)
+        });
+    }
+    // epilogue: lane holds output rows 4(l/16)..+4 of pick tt*16 + l%16
+    #pragma unroll
+    for (int tt = 0; tt < 8; ++tt)
+    {
+        const int pk = tt * 16 + row;
+        if (pk >= b.rows) continue;
+        #pragma unroll
+        for (int st = 0; st < NS; ++st)
+        {
+            const int n = (nb0 + st) * 16 + 4 * (l >> 4);
+            if (NMAT == 2)
+            {
+                const float wv = DENSE ? 1.0f : wt[b.p0 + pk];
+                _Float16 o[4];
+                #pragma unroll
+                for (int i = 0; i < 4; ++i) o[i] = (_Float16) (silu(acc[st][0][tt][i]) * acc[st][NMAT - 1][tt][i] * wv);
+                *(uint2*) (ar + (size_t) (off + b.p0 + pk) * NOUT + n) = *(const uint2*) o;
+            }
+            else *(f32x4*) (dout + (size_t) (off + b.p0 + pk) * NOUT + n) = acc[st][0][tt];
+        }
+    }
+}
+
+// x bf16 -> f16 (the GEMM input when the caller has no f16 copy)
+__global__ void __launch_bounds__(256) to_f16_kernel(const uint16_t* __restrict__ x, size_t n, _Float16* __restrict__ xh)
+{
+    for (size_t i = (blockIdx.x * (size_t) 256 + threadIdx.x) * 8; i < n; i += (size_t) gridDim.x * 256 * 8)
+    {
+        const u32x4 v = ld16(x + i);
         f16x8 o;
         #pragma unroll
         for (int k = 0; k < 4; ++k)
         {
-            o[2 * k] = (_Float16) __uint_as_float(v[q][k] << 16);
-            o[2 * k + 1] = (_Float16) __uint_as_float(v[q][k] & 0xffff0000u);
+            o[2 * k] = (_Float16) __uint_as_float(v[k] << 16);
+            o[2 * k + 1] = (_Float16) __uint_as_float(v[k] & 0xffff0000u);
         }
-        *(f16x8*) (xs + r * XSTR + c + 8 * q) = o;
-    }
-}
-__device__ __forceinline__ void load_x_f16(const _Float16* src_row, int k0, u32x4* v)
-{
-    #pragma unroll
-    for (int q = 0; q < 4; ++q) v[q] = src_row ? *(const u32x4*) (src_row + k0 + 8 * q) : (u32x4) {0u, 0u, 0u, 0u};
-}
-__device__ __forceinline__ void store_x_f16(_Float16* xs, const u32x4* v)
-{
-    const int t = threadIdx.x, r = t >> 2, c = (t & 3) * 32;
-    #pragma unroll
-    for (int q = 0; q < 4; ++q) *(u32x4*) (xs + r * XSTR + c + 8 * q) = v[q];
-}
-
-// A operand of one strip for one 128-k group: 4 k steps of 8 f16 per lane
-struct AFrag { f16x8 a[4]; };
-
-__device__ __forceinline__ void a_i4(const uint8_t* q, const uint8_t* s, int nb, int kg, int KG, AFrag& f)
-{
-    const int l = threadIdx.x & 63;
-    const u32x4 w = ldw16(q + ((size_t) (nb * KG + kg) * 64 + l) * 16);
-    const uint16_t sb = ldg<uint16_t>(s + ((size_t) (nb * 16 + (l & 15)) * KG + kg) * 2);
-    const _Float16 sh = (_Float16) bf2f(sb);
-    const f16x8 s8 = {sh, sh, sh, sh, sh, sh, sh, sh};
-    #pragma unroll
-    for (int t = 0; t < 4; ++t) f.a[t] = dq8(w[t]) * s8;
-}
-__device__ __forceinline__ void a_dense(const uint8_t* w, int nb, int kg, int KS, AFrag& f)
-{
-    const int l = threadIdx.x & 63;
-    #pragma unroll
-    for (int t = 0; t < 4; ++t) f.a[t] = as_f16x8(ldw16(w + ((size_t) (nb * KS + kg * 4 + t) * 64 + l) * 16));
-}
-
-// gate + up + act. DENSE: the shared expert over every token (block b = tokens [64 b, 64 b + 64), weight 1).
-template <bool DENSE>
-__global__ void __launch_bounds__(PT) pgu_kernel(
-    const uint16_t* __restrict__ x, const int* __restrict__ tok, const float* __restrict__ wt,
-    const int* __restrict__ rbt, int nrb, const int* __restrict__ meta, int n_tab,
-    const int64_t* __restrict__ gw, const int64_t* __restrict__ uw, const int64_t* __restrict__ gs,
-    const int64_t* __restrict__ us, const uint8_t* __restrict__ shg, const uint8_t* __restrict__ shu,
-    _Float16* __restrict__ ar, int T, int ar_off)
-{
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2][PB * XSTR];
-    Block b;
-    if (DENSE) { b.e = 0; b.p0 = blockIdx.x * PB; b.rows = min(PB, T - b.p0); if (b.rows <= 0) return; }
-    else if (!get_block(rbt, nrb, meta, n_tab, b)) return;
-    constexpr int KG = H / 128;
-    const int t = threadIdx.x, w = t >> 6, l = t & 63;
-    const int nb0 = blockIdx.y * (PN / 16) + 2 * w;            // strips nb0, nb0 + 1 of I / 16
-    const uint8_t *gq = nullptr, *uq = nullptr, *gsp = nullptr, *usp = nullptr;
-    if (!DENSE) { gq = (const uint8_t*) gw[b.e]; uq = (const uint8_t*) uw[b.e]; gsp = (const uint8_t*) gs[b.e]; usp = (const uint8_t*) us[b.e]; }
-    // this thread's staged input row
-    const int sr = t >> 2;
-    const uint16_t* src = nullptr;
-    if (sr < b.rows)
-    {
-        const int tk = DENSE ? b.p0 + sr : tok[b.p0 + sr];
-        if ((unsigned) tk < (unsigned) T) src = x + (size_t) tk * H + (t & 3) * 32;
-    }
-    const int ntt = (b.rows + 15) >> 4;
-    f32x4 acc[2][2][4];
-    #pragma unroll
-    for (int s = 0; s < 2; ++s)
-        #pragma unroll
-        for (int m = 0; m < 2; ++m)
-            #pragma unroll
-            for (int tt = 0; tt < 4; ++tt) acc[s][m][tt] = (f32x4) {0.f, 0.f, 0.f, 0.f};
-    u32x4 xv[4];
-    load_x_bf16(src, 0, xv);
-    for (int kg = 0; kg < KG; ++kg)
-    {
-        _Float16* xb = xs[kg & 1];
-        store_x_bf16(xb, xv);
-        __syncthreads();
-        if (kg + 1 < KG) load_x_bf16(src, (kg + 1) * 128, xv);
-        AFrag A[2][2];
-        #pragma unroll
-        for (int s = 0; s < 2; ++s)
-        {
-            if (DENSE) { a_dense(shg, nb0 + s, kg, H / 32, A[s][0]); a_dense(shu, nb0 + s, kg, H / 32, A[s][1]); }
-            else { a_i4(gq, gsp, nb0 + s, kg, KG, A[s][0]); a_i4(uq, usp, nb0 + s, kg, KG, A[s][1]); }
-        }
-        #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-        {
-            if (tt >= ntt) break;
-            const _Float16* bp = xb + (tt * 16 + (l & 15)) * XSTR + 8 * (l >> 4);
-            #pragma unroll
-            for (int k = 0; k < 4; ++k)
-            {
-                const f16x8 bv = *(const f16x8*) (bp + 32 * k);
-                #pragma unroll
-                for (int s = 0; s < 2; ++s)
-                    #pragma unroll
-                    for (int m = 0; m < 2; ++m) acc[s][m][tt] = mfma16(A[s][m].a[k], bv, acc[s][m][tt]);
-            }
-        }
-    }
-    // epilogue: lane holds rows 4(l/16)..+4 of pick tt*16 + l%16
-    #pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-    {
-        const int pk = tt * 16 + (l & 15);
-        if (pk >= b.rows) continue;
-        const float wv = DENSE ? 1.0f : wt[b.p0 + pk];
-        #pragma unroll
-        for (int s = 0; s < 2; ++s)
-        {
-            const int n = (nb0 + s) * 16 + 4 * (l >> 4);
-            _Float16 o[4];
-            #pragma unroll
-            for (int i = 0; i < 4; ++i) o[i] = (_Float16) (silu(acc[s][0][tt][i]) * acc[s][1][tt][i] * wv);
-            *(uint2*) (ar + (size_t) (ar_off + b.p0 + pk) * I + n) = *(const uint2*) o;
-        }
-    }
-}
-
-// down: d[pick] = W_d act[pick] (fp32)
-template <bool DENSE>
-__global__ void __launch_bounds__(PT) pdown_kernel(
-    const _Float16* __restrict__ ar, const int* __restrict__ rbt, int nrb, const int* __restrict__ meta, int n_tab,
-    const int64_t* __restrict__ dw, const int64_t* __restrict__ ds, const uint8_t* __restrict__ shd,
-    float* __restrict__ d, int T, int off)
-{
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2][PB * XSTR];
-    Block b;
-    if (DENSE) { b.e = 0; b.p0 = blockIdx.x * PB; b.rows = min(PB, T - b.p0); if (b.rows <= 0) return; }
-    else if (!get_block(rbt, nrb, meta, n_tab, b)) return;
-    constexpr int KG = I / 128;
-    const int t = threadIdx.x, w = t >> 6, l = t & 63;
-    const int nb0 = blockIdx.y * (PN / 16) + 2 * w;
-    const uint8_t *dq = nullptr, *dsp = nullptr;
-    if (!DENSE) { dq = (const uint8_t*) dw[b.e]; dsp = (const uint8_t*) ds[b.e]; }
-    const int sr = t >> 2;
-    const _Float16* src = sr < b.rows ? ar + (size_t) (off + b.p0 + sr) * I + (t & 3) * 32 : nullptr;
-    const int ntt = (b.rows + 15) >> 4;
-    f32x4 acc[2][4];
-    #pragma unroll
-    for (int s = 0; s < 2; ++s)
-        #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) acc[s][tt] = (f32x4) {0.f, 0.f, 0.f, 0.f};
-    u32x4 xv[4];
-    load_x_f16(src, 0, xv);
-    for (int kg = 0; kg < KG; ++kg)
-    {
-        _Float16* xb = xs[kg & 1];
-        store_x_f16(xb, xv);
-        __syncthreads();
-        if (kg + 1 < KG) load_x_f16(src, (kg + 1) * 128, xv);
-        AFrag A[2];
-        #pragma unroll
-        for (int s = 0; s < 2; ++s)
-        {
-            if (DENSE) a_dense(shd, nb0 + s, kg, I / 32, A[s]);
-            else a_i4(dq, dsp, nb0 + s, kg, KG, A[s]);
-        }
-        #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-        {
-            if (tt >= ntt) break;
-            const _Float16* bp = xb + (tt * 16 + (l & 15)) * XSTR + 8 * (l >> 4);
-            #pragma unroll
-            for (int k = 0; k < 4; ++k)
-            {
-                const f16x8 bv = *(const f16x8*) (bp + 32 * k);
-                #pragma unroll
-                for (int s = 0; s < 2; ++s) acc[s][tt] = mfma16(A[s].a[k], bv, acc[s][tt]);
-            }
-        }
-    }
-    #pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-    {
-        const int pk = tt * 16 + (l & 15);
-        if (pk >= b.rows) continue;
-        #pragma unroll
-        for (int s = 0; s < 2; ++s)
-        {
-            const int n = (nb0 + s) * 16 + 4 * (l >> 4);
-            *(f32x4*) (d + (size_t) (off + b.p0 + pk) * H + n) = acc[s][tt];
-        }
+        *(f16x8*) (xh + i) = o;
     }
 }
 
@@ -382,7 +385,7 @@ extern "C" size_t hmoe_moe4p_scratch_bytes(int which, int ps, int T)
 {
     switch (which)
     {
-        case 0: return 16;                                              // gu: unused (gate/up fused with act)
+        case 0: return (size_t) T * H * 2;                              // gu: the f16 copy of x (when xf = 0)
         case 1: return (size_t) (ps + T) * I * 2;                       // ar f16 [ps + T][I]
         case 2: return (size_t) (ps + T) * H * 4;                       // d fp32 [ps + T][H]
         default: return 0;
@@ -393,9 +396,9 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
                                   int npos, int nrb, int n_tab, const int64_t* gw, const int64_t* uw, const int64_t* dw,
                                   const int64_t* gs, const int64_t* us, const int64_t* ds, float* gu, uint16_t* ar,
                                   float* d, float* out, int ps, const int* meta, const int* inv, int T, int topk,
-                                  const void* sh_gw, const void* sh_uw, const void* sh_dw, void* stream)
+                                  const void* sh_gw, const void* sh_uw, const void* sh_dw, int xf, void* stream)
 {
-    (void) gu; (void) eid;
+    (void) eid;
     HMOE_REQUIRE(x && tok && wt && rbt && ar && d && out, "moe4p_forward: null buffer");
     HMOE_REQUIRE(npos >= 0 && nrb >= 0 && npos <= ps && T >= 1 && topk >= 1 && topk <= TOPK,
                  "moe4p_forward: npos %d nrb %d ps %d T %d topk %d", npos, nrb, ps, T, topk);
@@ -406,22 +409,34 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
                  ((uintptr_t) out & 15) == 0, "moe4p_forward: alignment");
     hipStream_t st = (hipStream_t) stream;
     const uint16_t* xb = (const uint16_t*) x;
+    if (!xf)
+    {
+        HMOE_REQUIRE(gu && ((uintptr_t) gu & 15) == 0, "moe4p_forward: xf = 0 needs the gu scratch (the f16 copy of x)");
+        to_f16_kernel<<<1024, 256, 0, st>>>(xb, (size_t) T * H, (_Float16*) gu);
+        xb = (const uint16_t*) gu;
+    }
     _Float16* a = (_Float16*) ar;
+    // gate/up: 64 x 2 output columns per workgroup (NS 2); down: 64 x 4 (NS 4)
     if (nrb > 0)
     {
-        pgu_kernel<false><<<dim3(nrb, I / PN), PT, 0, st>>>(xb, tok, wt, rbt, nrb, meta, n_tab, gw, uw, gs, us, nullptr,
-                                                           nullptr, a, T, 0);
-        pdown_kernel<false><<<dim3(nrb, H / PN), PT, 0, st>>>(a, rbt, nrb, meta, n_tab, dw, ds, nullptr, d, T, 0);
+        pgemm_kernel<false, 2, 2, 3><<<dim3(nrb, I / 128), PT, 0, st>>>((const _Float16*) xb, tok, wt, rbt, nrb, meta, n_tab, gw, uw,
+                                                                             gs, us, nullptr, nullptr, a, nullptr, T, 0);
+        pgemm_kernel<false, 1, 4, 2><<<dim3(nrb, H / 256), PT, 0, st>>>(a, nullptr, nullptr, rbt,
+                                                                               nrb, meta, n_tab, dw, nullptr, ds, nullptr,
+                                                                               nullptr, nullptr, nullptr, d, T, 0);
     }
     const bool sh = sh_gw != nullptr;
     if (sh)
     {
         const int nbk = (T + PB - 1) / PB;
-        pgu_kernel<true><<<dim3(nbk, I / PN), PT, 0, st>>>(xb, nullptr, nullptr, nullptr, 0, nullptr, 1, nullptr, nullptr,
-                                                          nullptr, nullptr, (const uint8_t*) sh_gw, (const uint8_t*) sh_uw,
-                                                          a, T, ps);
-        pdown_kernel<true><<<dim3(nbk, H / PN), PT, 0, st>>>(a, nullptr, 0, nullptr, 1, nullptr, nullptr,
-                                                            (const uint8_t*) sh_dw, d, T, ps);
+        pgemm_kernel<true, 2, 2, 1><<<dim3(nbk, I / 128), PT, 0, st>>>((const _Float16*) xb, nullptr, nullptr, nullptr, 0, nullptr, 1,
+                                                                            nullptr, nullptr, nullptr, nullptr,
+                                                                            (const uint8_t*) sh_gw, (const uint8_t*) sh_uw,
+                                                                            a, nullptr, T, ps);
+        pgemm_kernel<true, 1, 4, 1><<<dim3(nbk, H / 256), PT, 0, st>>>(a, nullptr, nullptr,
+                                                                             nullptr, 0, nullptr, 1, nullptr, nullptr,
+                                                                             nullptr, nullptr, (const uint8_t*) sh_dw,
+                                                                             nullptr, nullptr, d, T, ps);
     }
     if (inv) pfin_kernel<<<T, 256, 0, st>>>(d, inv, topk, sh ? ps : -1, out);
     else if (npos > 0) pfin_atomic_kernel<<<npos, 256, 0, st>>>(d, tok, npos, meta, T, out);

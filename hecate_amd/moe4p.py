@@ -12,7 +12,8 @@ H, I = 6144, 2048
 
 
 def scratch(dev, npos, T=0):
-    """moe4p.cu:209-215: [gu, ar, d] for up to npos picks (+ T rows for the shared expert)"""
+    """moe4p.cu:209-215: [gu, ar, d] for up to npos picks (+ T rows for the shared expert); gu holds the f16 copy of
+    x when forward gets bf16 x"""
     dev = torch.device(dev)
     L = lib()
     return [torch.zeros(int(L.hmoe_moe4p_scratch_bytes(0, npos, T)) // 4, dtype=torch.float32, device=dev),
@@ -22,9 +23,11 @@ def scratch(dev, npos, T=0):
 
 def forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, inv=None, meta=None, topk=8, shared=None,
             npos=None, nrb=None):
-    """moe4p.cu:220-245: out[tok] += routed experts of the sorted picks (+ the shared expert on every token)"""
+    """moe4p.cu:220-245: out[tok] += routed experts of the sorted picks (+ the shared expert on every token); x bf16, or
+    its f16 copy (as router_fused writes it)"""
     T = x.shape[0]
-    if not (x.dim() == 2 and x.shape[1] == H and x.dtype == torch.bfloat16 and out.dtype == torch.float32
+    xf = 1 if x.dtype == torch.float16 else 0
+    if not (x.dim() == 2 and x.shape[1] == H and x.dtype in (torch.bfloat16, torch.float16) and out.dtype == torch.float32
             and rbt.dim() == 2 and rbt.shape[1] == 4 and x.is_contiguous() and out.is_contiguous()):
         raise RuntimeError("moe4p: shapes")
     npos = tok.numel() if npos is None else npos
@@ -35,4 +38,4 @@ def forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, inv=No
     sh = shared if shared is not None else (None, None, None)
     call("hmoe_moe4p_forward", ptr(x), ptr(tok), ptr(eid), ptr(wt), ptr(rbt), int(npos), int(nrb), gw.numel(),
          ptr(gw), ptr(uw), ptr(dw), ptr(gs), ptr(us), ptr(ds), ptr(gu), ptr(ar), ptr(d), ptr(out), int(ps),
-         ptr(meta), ptr(inv), int(T), int(topk), ptr(sh[0]), ptr(sh[1]), ptr(sh[2]), stream_of(x.device))
+         ptr(meta), ptr(inv), int(T), int(topk), ptr(sh[0]), ptr(sh[1]), ptr(sh[2]), xf, stream_of(x.device))

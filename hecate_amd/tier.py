@@ -81,7 +81,7 @@ class ExpertBank:
 class PrefillBuffers:
     """device buffers of a prefill chunk of up to T rows: selection, dispatch plan (hmoe_dispatch), GEMM scratch"""
 
-    def __init__(self, T, topk, lo, n, E, device, bm=64):
+    def __init__(self, T, topk, lo, n, E, device, bm=128):
         dev = torch.device(device)
         L = lib()
         self.T, self.topk, self.lo, self.n, self.bm = T, topk, lo, n, bm
@@ -95,10 +95,11 @@ class PrefillBuffers:
         self.scr = moe4p.scratch(dev, F, T)
         self.y = z(T, H, dt=torch.float32)
         self.out = z(T, H, dt=torch.bfloat16)
+        self.xh = z(T, H, dt=torch.float16)                        # the router's f16 copy of x (the GEMM input)
         self.sel, self.rw = z(T, topk, dt=torch.int64), z(T, topk, dt=torch.float16)
         self.logits = z(int(L.hmoe_router_scratch_bytes(T, E)) // 4, dt=torch.float32)
 
-    def run(self, sel, rw, balance=False):
+    def run(self, sel, rw, balance=True):
         """device dispatch plan of a selection (tier_split.py:404-417 + pick_groups in one group), no host sync:
         counts, tok / eid / wt sorted by (expert, flat index), inv, rbt rows, meta = {npos, nrb, nrb wanted, 0}"""
         T = sel.shape[0]
@@ -195,10 +196,10 @@ class MoELayer:
         T = x.shape[0]
         pf = self._prefill_buffers(T)
         sel, rw = pf.sel[:T], pf.rw[:T]
-        router.router_fused(x, self.wg, self.bias, pf.logits, self.ctr, sel, rw, self.topk, self.scale)
+        router.router_fused(x, self.wg, self.bias, pf.logits, self.ctr, sel, rw, self.topk, self.scale, pf.xh[:T])
         pf.run(sel, rw)
         y = pf.y[:T]
-        self.prefill_experts(x, y, with_shared)
+        self.prefill_experts(pf.xh[:T], y, with_shared)
         return moe4.finish_bf16(y, T, pf.out[:T])
 
     def forward(self, x):

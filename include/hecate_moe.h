@@ -135,10 +135,12 @@ int hmoe_dispatch(const int64_t* sel, const uint16_t* rw, int T, int topk, int l
 
 /* ---- prefill: runtime/tier/moe4/moe4p.cu:217-245 moe4p_forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar,
  * d, out) ----
- * x bf16 [T][H]; tok int32 [npos] (token of each pick), eid int32 [npos] (not read: the expert of a row block is in
- * rbt), wt fp32 [npos]; rbt int32 [nrb][4] rows {expert (relative to the tables), first pick, picks <= 64, 0};
+ * x bf16 [T][H] (xf = 0) or its f16 copy (xf = 1, as router_fused writes it); tok int32 [npos] (token of each pick),
+ * eid int32 [npos] (not read: the expert of a row block is in
+ * rbt), wt fp32 [npos]; rbt int32 [nrb][4] rows {expert (relative to the tables), first pick, picks <= 128, 0};
  * tables (n_tab entries) as in hmoe_moe4_forward; ar f16 [ps + T][I] and d fp32 [ps + T][H] scratch
- * (hmoe_moe4p_scratch_bytes); gu unused (NULL allowed); out fp32 [T][H] accumulated into. meta: NULL, or the device
+ * (hmoe_moe4p_scratch_bytes); gu: room for the f16 copy of x [T][H] when xf = 0 (else unused, NULL allowed); out
+ * fp32 [T][H] accumulated into. meta: NULL, or the device
  * {npos, nrb} written by hmoe_dispatch (then npos / nrb are the static maxima the grids are sized for). inv: NULL
  * (picks added with atomics, as p4_fin_kernel) or the dispatch's inverse map (each token's picks added in top-k
  * order: deterministic). sh_*: the shared expert as F16T or NULL (needs inv); it runs on every token with weight 1. */
@@ -147,7 +149,7 @@ int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid, const floa
                        int nrb, int n_tab, const int64_t* gw, const int64_t* uw, const int64_t* dw, const int64_t* gs,
                        const int64_t* us, const int64_t* ds, float* gu, uint16_t* ar, float* d, float* out, int ps,
                        const int* meta, const int* inv, int T, int topk, const void* sh_gw, const void* sh_uw,
-                       const void* sh_dw, void* stream);
+                       const void* sh_dw, int xf, void* stream);
 
 /* ---- residual + RMSNorm between layers: runtime/tier/cn.cu:48-103 (combine_norm) restated for fp32 weights ----
  * r fp32 [R][H] residual += a (a fp32 [R][H] or NULL; a is zeroed after use), xn = bf16(r * rsqrt(mean r^2 + eps) * w)
