@@ -119,10 +119,11 @@ __global__ void dequant_kernel(const u32x4* __restrict__ q, const uint16_t* __re
         const int row = nb * 16 + (l & 15);
         const float sc = bf2f(s[(size_t) row * KG + kg]);
         const u32x4 v = q[i];
+        const DqConsts dq = dq_consts();
         #pragma unroll
         for (int j = 0; j < 4; ++j)
         {
-            const f16x8 d = dq8(v[j]);
+            const f16x8 d = dq8(v[j], dq);
             const int k0 = kg * 128 + 32 * j + 8 * (l >> 4);
             #pragma unroll
             for (int e = 0; e < 8; ++e) out[(size_t) row * K + k0 + e] = (_Float16) ((float) d[e] * sc);

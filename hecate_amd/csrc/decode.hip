@@ -96,11 +96,11 @@ __device__ __forceinline__ f16x8 bf8_to_f16(u32x4 v)
 }
 
 // one 128-k group of an I4G128 tile (weights as the B operand) against 4 k steps of token rows: scaled into acc
-__device__ __forceinline__ void group_i4(const f16x8* xa, u32x4 wq, float s, f32x4& acc)
+__device__ __forceinline__ void group_i4(const f16x8* xa, u32x4 wq, float s, f32x4& acc, const DqConsts& dq)
 {
     f32x4 p = {0.f, 0.f, 0.f, 0.f};
     #pragma unroll
-    for (int t = 0; t < 4; ++t) p = mfma16(xa[t], dq8(wq[t]), p);
+    for (int t = 0; t < 4; ++t) p = mfma16(xa[t], dq8(wq[t], dq), p);
     #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(s, p[i], acc[i]);
 }
@@ -168,6 +168,7 @@ __global__ void __launch_bounds__(GW * 64) gu5_kernel(
     const int nmine = (int) blockIdx.x < total ? (total - 1 - (int) blockIdx.x) / G + 1 : 0;
     if (nmine == 0) return;                                    // uniform over the workgroup
     const int row = l & 15;
+    const DqConsts dq = dq_consts();
     auto load = [&](GuItem& S, int i) {
         const int it = blockIdx.x + i * G, j = it / NB_I, nb = it - j * NB_I;
         const size_t toff = ((size_t) (nb * KG_H + 4 * w) * 64 + l) * 16;
@@ -186,8 +187,8 @@ __global__ void __launch_bounds__(GW * 64) gu5_kernel(
         #pragma unroll
         for (int k = 0; k < 4; ++k)
         {
-            group_i4(xa + 4 * k, S.g[k], scale_of(S.sg, k), ag);
-            group_i4(xa + 4 * k, S.u[k], scale_of(S.su, k), au);
+            group_i4(xa + 4 * k, S.g[k], scale_of(S.sg, k), ag, dq);
+            group_i4(xa + 4 * k, S.u[k], scale_of(S.su, k), au, dq);
         }
         red[par][w][0][l] = ag; red[par][w][1][l] = au;
         __syncthreads();
@@ -250,6 +251,7 @@ __global__ void __launch_bounds__(DW * 64) dn5_kernel(
     const bool live = tok < R;
     f16x8 xa[16];
     int cur_q = -1;
+    const DqConsts dq = dq_consts();
     auto load = [&](DnItem& S, int i) {
         const int it = i0 + i, qd = it / NB_H, nb = it - qd * NB_H, j = 4 * qd + sw;
         // a slot past m loads one fixed tile of slot m - 1 (the same load count on every path, no HBM traffic)
@@ -279,7 +281,7 @@ __global__ void __launch_bounds__(DW * 64) dn5_kernel(
         }
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         #pragma unroll
-        for (int k = 0; k < 4; ++k) group_i4(xa + 4 * k, S.d[k], scale_of(S.s, k), acc);
+        for (int k = 0; k < 4; ++k) group_i4(xa + 4 * k, S.d[k], scale_of(S.s, k), acc, dq);
         red[par][w][l] = acc;
         __syncthreads();
         if (threadIdx.x < 256)

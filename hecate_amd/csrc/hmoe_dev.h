@@ -39,24 +39,43 @@ __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint
 // 8 codes of one I4G128 dword -> 8 exact f16 values q = code - 8, element e of the MFMA operand at nibble bit
 // 4(e/2) + 16(e%2): (code | 0x6400) is the f16 1024 + code (0x6400 = 1024, one unit per mantissa step), minus 1032;
 // the odd nibble of each byte lands 4 bits up, 1024 + 16 code, scaled by 1/16 and offset by -72 (all exact).
-// The masks and the exponent sit in registers the compiler cannot fold into literals, so each (w & mask) | 0x6400..
-// is one v_and_or_b32 (a VOP3 of gfx9 takes no 32-bit literal, and two literals would cost two instructions).
-__device__ __forceinline__ f16x8 dq8(uint32_t w)
+// The two masks and the exponent live in registers made once per kernel (dq_consts): (w & mask) | 0x6400.. is then
+// one v_and_or_b32 (a VOP3 of gfx9 takes no 32-bit literal; with literals it costs two instructions).
+struct DqConsts { uint32_t m0, m1, mg; };
+__device__ __forceinline__ DqConsts dq_consts()
 {
-    uint32_t m0 = 0x000f000fu, m1 = 0x00f000f0u, mg = 0x64006400u;
-    asm volatile("" : "+v"(m0), "+v"(m1), "+v"(mg));
+    DqConsts c = {0x000f000fu, 0x00f000f0u, 0x64006400u};
+    asm volatile("" : "+v"(c.m0), "+v"(c.m1), "+v"(c.mg));
+    return c;
+}
+
+__device__ __forceinline__ f16x8 dq8(uint32_t w, const DqConsts& c)
+{
     const uint32_t top = w >> 8;
-    const uint32_t h0 = (w & m0) | mg;
-    const uint32_t h1 = (w & m1) | mg;
-    const uint32_t h2 = (top & m0) | mg;
-    const uint32_t h3 = (top & m1) | mg;
     const f16x2 m1032 = {(_Float16) -1032.0f, (_Float16) -1032.0f};
     const f16x2 s16 = {(_Float16) 0.0625f, (_Float16) 0.0625f};
     const f16x2 m72 = {(_Float16) -72.0f, (_Float16) -72.0f};
-    const f16x2 a0 = __builtin_bit_cast(f16x2, h0) + m1032;
-    const f16x2 a1 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, h1), s16, m72);
-    const f16x2 a2 = __builtin_bit_cast(f16x2, h2) + m1032;
-    const f16x2 a3 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, h3), s16, m72);
+    const f16x2 a0 = __builtin_bit_cast(f16x2, (w & c.m0) | c.mg) + m1032;
+    const f16x2 a1 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (w & c.m1) | c.mg), s16, m72);
+    const f16x2 a2 = __builtin_bit_cast(f16x2, (top & c.m0) | c.mg) + m1032;
+    const f16x2 a3 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (top & c.m1) | c.mg), s16, m72);
+    f16x8 r;
+    r[0] = a0[0]; r[1] = a0[1]; r[2] = a1[0]; r[3] = a1[1];
+    r[4] = a2[0]; r[5] = a2[1]; r[6] = a3[0]; r[7] = a3[1];
+    return r;
+}
+
+// dq8 times a per-row f16 scale pair {s, s}: f16((code - 8) * s) (exact codes, one rounding)
+__device__ __forceinline__ f16x8 dq8s(uint32_t w, f16x2 ss, const DqConsts& c)
+{
+    const uint32_t top = w >> 8;
+    const f16x2 m1032 = {(_Float16) -1032.0f, (_Float16) -1032.0f};
+    const f16x2 s16 = {(_Float16) 0.0625f, (_Float16) 0.0625f};
+    const f16x2 m72 = {(_Float16) -72.0f, (_Float16) -72.0f};
+    const f16x2 a0 = (__builtin_bit_cast(f16x2, (w & c.m0) | c.mg) + m1032) * ss;
+    const f16x2 a1 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (w & c.m1) | c.mg), s16, m72) * ss;
+    const f16x2 a2 = (__builtin_bit_cast(f16x2, (top & c.m0) | c.mg) + m1032) * ss;
+    const f16x2 a3 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (top & c.m1) | c.mg), s16, m72) * ss;
     f16x8 r;
     r[0] = a0[0]; r[1] = a0[1]; r[2] = a1[0]; r[3] = a1[1];
     r[4] = a2[0]; r[5] = a2[1]; r[6] = a3[0]; r[7] = a3[1];

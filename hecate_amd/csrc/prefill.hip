@@ -142,7 +142,8 @@ __global__ void __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(2))) pg
     Block b;
     if (DENSE) { b.e = 0; b.p0 = blockIdx.x * PB; b.rows = min(PB, T - b.p0); if (b.rows <= 0) return; }
     else if (!get_block(rbt, nrb, meta, n_tab, b)) return;
-    const int t = threadIdx.x, w = t >> 6, l = t & 63, row = l & 15;
+    const int t = threadIdx.x, l = t & 63, row = l & 15;
+    const int w = __builtin_amdgcn_readfirstlane(t >> 6);   // wave index, kept in a scalar register
     const int nb0 = (blockIdx.y * 4 + w) * NS;
     const uint8_t* wp[NMAT];
     const uint8_t* sp[NMAT];
@@ -153,6 +154,7 @@ __global__ void __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(2))) pg
         sp[m] = DENSE ? nullptr : (const uint8_t*) (m == 0 ? s0 : s1)[b.e];
     }
     const int ntt = (b.rows + 15) >> 4;
+    const DqConsts dq = dq_consts();
     // wave w stages tiles 2w and 2w + 1: lane l's source row; a pick past the block re-reads a valid row (its output
     // columns are never stored), a whole tile past the block reads one fixed 16 bytes
     const _Float16* src[2];
@@ -240,11 +242,15 @@ __global__ void __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(2))) pg
             else asm volatile("s_waitcnt vmcnt(%0)" :: "n"(FETCH_LOADS) : "memory");
             __syncthreads();
             if (kg + 1 < KG) stage(kg + 1, even ? xs1 : xs0);
-            _Float16 sh[NS][NMAT];
+            f16x2 sh[NS][NMAT];
             #pragma unroll
             for (int st = 0; st < NS; ++st)
                 #pragma unroll
-                for (int m = 0; m < NMAT; ++m) sh[st][m] = DENSE ? (_Float16) 1.0f : (_Float16) bf2f(ring[s].s[st][m]);
+                for (int m = 0; m < NMAT; ++m)
+                {
+                    const _Float16 h = DENSE ? (_Float16) 1.0f : (_Float16) bf2f(ring[s].s[st][m]);
+                    sh[st][m] = (f16x2) {h, h};
+                }
             #pragma unroll
             for (int k = 0; k < 4; ++k)
             {
@@ -253,15 +259,7 @@ __global__ void __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(2))) pg
                 for (int st = 0; st < NS; ++st)
                     #pragma unroll
                     for (int m = 0; m < NMAT; ++m)
-                    {
-                        if (DENSE) a[st][m] = as_f16x8(ring[s].q[st][m][k]);
-                        else
-                        {
-                            const _Float16 h = sh[st][m];
-                            const f16x8 s8 = {h, h, h, h, h, h, h, h};
-                            a[st][m] = dq8(ring[s].q[st][m][0][k]) * s8;
-                        }
-                    }
+                        a[st][m] = DENSE ? as_f16x8(ring[s].q[st][m][k]) : dq8s(ring[s].q[st][m][0][k], sh[st][m], dq);
                 #pragma unroll
                 for (int tt = 0; tt < 8; ++tt)
                 {
