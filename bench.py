@@ -291,9 +291,9 @@ def main():
         return
     cpu = None if args.no_cpu else cpu_baseline()
     kb = head["kernels"]["B_routed_gate_up"]
-    roof = {"bound": "hbm", "kernel": "dec_b_kernel (routed int4 gate/up + SwiGLU)",
+    roof = {"bound": "hbm", "kernel": "gu5_kernel (top-8 selection + routed int4 gate/up + SwiGLU)",
             "achieved": kb["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": kb["gbs"] / HBM_PEAK_GBS,
-            "traffic": traffic_from_profiles("dec_b_kernel"), "algorithmic_bytes_per_launch": kb["algorithmic_bytes"],
+            "traffic": traffic_from_profiles("gu5_kernel"), "algorithmic_bytes_per_launch": kb["algorithmic_bytes"],
             "launch_us": kb["us"]}
     extra["decode_b16"] = head
     line = {"metric": metric_name(), "value": head["tok_per_s"], "unit": "tok/s", "n_gpus": 1, "steps": K,
