@@ -73,8 +73,8 @@ def decode_workload(torch, synth, R, steps, warmup, zipf, dev, n_layers=6, n_x=6
         f"{time.perf_counter() - t0:.1f} s")
     L, P = len(layers), len(xs)
     el = timed(torch, lambda i: layers[i % L].decode(xs[i % P]), steps, warmup)
-    # per-kernel timing of the same steps with HIP events on the launch stream: A (router logits + shared gate/up),
-    # B (routed gate/up + SwiGLU), C (down), D (ordered reduce + bf16 out)
+    # per-kernel timing of the same steps with HIP events on the launch stream: A (router logits), B (shared + routed
+    # gate/up + SwiGLU, gu7_kernel), C (shared + routed down, dn6_kernel), D (ordered reduce + bf16 out)
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
     for i in range(steps):
         lay, x = layers[i % L], xs[i % P]
@@ -93,11 +93,11 @@ def decode_workload(torch, synth, R, steps, warmup, zipf, dev, n_layers=6, n_x=6
     U = np.array(U, np.float64)
     step_s = el / steps
     bytes_step = float(np.mean(U * EXPERT_BYTES + SHARED_BYTES + ROUTER_BYTES + R * 2 * H * 2))
-    kbytes = [ROUTER_BYTES + SHARED_GU_BYTES + R * H * 2,
-              float(np.mean(U * GU_EXPERT_BYTES + R * H * 2)),
+    kbytes = [ROUTER_BYTES + R * H * 2,
+              float(np.mean(U * GU_EXPERT_BYTES + SHARED_GU_BYTES + R * H * 2)),
               float(np.mean(U * DOWN_EXPERT_BYTES + SHARED_DOWN_BYTES + (U + 1) * R * 2048 * 2)),
               0.0]
-    names = ["A_router_shared_gate_up", "B_routed_gate_up", "C_down", "D_reduce_out"]
+    names = ["A_router", "B_gate_up", "C_down", "D_reduce_out"]
     res = {"rows": R, "us_per_step": step_s * 1e6, "us_per_token": step_s * 1e6 / R, "tok_per_s": R / step_s,
            "distinct_experts_mean": float(U.mean()), "bytes_per_step": bytes_step,
            "hbm_gbs": bytes_step / step_s / 1e9, "hbm_frac": bytes_step / step_s / 1e9 / HBM_PEAK_GBS,
@@ -290,10 +290,10 @@ def main():
         print(json.dumps({"extra": extra}))
         return
     cpu = None if args.no_cpu else cpu_baseline()
-    kb = head["kernels"]["B_routed_gate_up"]
-    roof = {"bound": "hbm", "kernel": "gu5_kernel (top-8 selection + routed int4 gate/up + SwiGLU)",
+    kb = head["kernels"]["B_gate_up"]
+    roof = {"bound": "hbm", "kernel": "gu7_kernel (shared gate/up + top-8 selection + routed int4 gate/up + SwiGLU)",
             "achieved": kb["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": kb["gbs"] / HBM_PEAK_GBS,
-            "traffic": traffic_from_profiles("gu5_kernel"), "algorithmic_bytes_per_launch": kb["algorithmic_bytes"],
+            "traffic": traffic_from_profiles("gu7_kernel"), "algorithmic_bytes_per_launch": kb["algorithmic_bytes"],
             "launch_us": kb["us"]}
     extra["decode_b16"] = head
     line = {"metric": metric_name(), "value": head["tok_per_s"], "unit": "tok/s", "n_gpus": 1, "steps": K,

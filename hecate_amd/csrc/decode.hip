@@ -5,6 +5,7 @@
 //   * the only vector-memory loads in a streaming loop are the 1 KB weight tiles (one 16-byte load per lane); group
 //     scales come 4 k groups per load, and the activations stay in registers for the whole kernel: every extra vector
 //     load per tile (a scale, an activation fragment from L2) costs 15-30 % of the achieved HBM bandwidth;
+//   * the expert pointer tables go to LDS at kernel start, so the routing prologue ends in LDS reads;
 //   * loads are unconditional and double-buffered per item (ping-pong between two register sets), so every wait
 //     counts exactly and the next item's tiles are in flight across the item's reduction barrier;
 //   * no workgroup waits for another inside a launch (on gfx950 an agent-scope fence writes back and invalidates
@@ -14,21 +15,24 @@
 // operand (32 k x 16 weight rows), so a lane's outputs share one weight row n = l % 16 and one group scale:
 // lane l holds D[tokens 4(l/16)..+4][row l%16].
 //
-// Launches (main stream; the shared expert runs on a side stream, joined before the reduction):
+// Launches (on the caller's stream):
 //   router   logits of two experts per workgroup (fixed fp32 order, see hecate_moe.h)
-//   gate/up  every workgroup derives the step's routing (top-k from the logits, or the given sel / rw) and the
-//            distinct experts (moe4.cu:86-110), then takes items (slot, 16-row block nb) b, b + G, ...; 12 waves each
-//            own 4 k groups of H with the rows' x in registers; the 12 wave partials are summed in wave order through
-//            LDS and act[slot][r][n] = f16(silu(g) u w) is written (moe4.cu:645-676)
-//   down     items (slot quad, 16-row block of H), contiguous per workgroup; 16 waves = 4 slots x 4 k quarters of I
-//            with the slots' act in registers; the 16 partials are summed in order into y32[part] (moe4.cu:443-643)
+//   gate/up  256 workgroups; each first sums one matrix (gate or up) of one 16-row block of the shared expert over
+//            the full K (its loads go out before the routing prologue and cover it; fp32 sums into act), then
+//            derives the step's routing (top-k from the logits, or the given sel / rw) and the distinct experts
+//            (moe4.cu:86-110) and takes routed items (slot, 16-row block nb) b, b + G, ...; 12 waves each own 4 k
+//            groups of H with the rows' x in registers; the 12 wave partials are summed in wave order through LDS
+//            and act[slot][r][n] = f16(silu(g) u w) is written (moe4.cu:645-676)
+//   down     first the shared expert's 16-row blocks of H (part 0, its act formed from the fp32 sums; no routing
+//            needed, so their loads cover the routing prologue), then routed items (slot quad, 16-row block of H),
+//            contiguous per workgroup; 16 waves = 4 slots x 4 k quarters of I with the slots' act in registers; the
+//            16 partials are summed in order into y32[part] (moe4.cu:443-643)
 //   reduce   y[r] (+)= sum of the parts in order (moe4.cu:826-827 accumulates into y), or the layer's bf16 output
-//   side     shared gate/up (F16T, act slot SH_SLOT, weight 1), shared down (part 0)
 #include "hmoe_dev.h"
 
 namespace hmoe {
 
-constexpr int NW = 8, NT = NW * 64;        // router / shared gate-up workgroup
+constexpr int NW = 8, NT = NW * 64;        // router workgroup
 constexpr int KG_H = H / 128;              // 48 k groups of gate / up
 constexpr int KG_I = I / 128;              // 16 k groups of down
 constexpr int NB_I = I / 16;               // 128 row blocks of gate / up
@@ -48,9 +52,19 @@ struct Route
     float w[MAXSLOT][MAXR];
 };
 
+// the raw pick of thread t < R * TOPK (sel, rw), read from GLOBAL memory (global address space loads: sel / rw must
+// not be in LDS). The loads are unconditional (index clamped), so a caller can issue them ahead of its weight loads
+// and consume them later.
+struct Pick { int64_t s; uint16_t w; };
+__device__ __forceinline__ Pick load_pick_global(const int64_t* sel, const uint16_t* rw, int R)
+{
+    const int i = min((int) threadIdx.x, R * TOPK - 1);
+    return {ldg<int64_t>(sel + i), ldg<uint16_t>(rw + i)};
+}
+
 // distinct experts of the step (ascending local id) and routing weight per (slot, row): moe4.cu:86-110, with the slot
-// of each pick from popcounts of the 256-bit mask. sel / rw may be in LDS or global memory. Ends with a barrier.
-__device__ void route(const int64_t* sel, const uint16_t* rw, int R, int lo, int n_hot, Route& rt)
+// of each pick from popcounts of the 256-bit mask. Ends with a barrier.
+__device__ void route_picks(Pick pk, int R, int lo, int n_hot, Route& rt)
 {
     const int t = threadIdx.x, np = R * TOPK;
     if (t < 8) rt.mask[t] = 0u;
@@ -58,8 +72,8 @@ __device__ void route(const int64_t* sel, const uint16_t* rw, int R, int lo, int
     int e = -1; float wv = 0.f;
     if (t < np)
     {
-        const int64_t s = sel[t] - lo;
-        if (s >= 0 && s < n_hot) { e = (int) s; wv = (float) __builtin_bit_cast(_Float16, rw[t]); }
+        const int64_t s = pk.s - lo;
+        if (s >= 0 && s < n_hot) { e = (int) s; wv = (float) __builtin_bit_cast(_Float16, pk.w); }
     }
     __syncthreads();
     if (e >= 0) atomicOr(&rt.mask[e >> 5], 1u << (e & 31));
@@ -73,6 +87,13 @@ __device__ void route(const int64_t* sel, const uint16_t* rw, int R, int lo, int
     }
     if (t == 0) { int m = 0; for (int wd = 0; wd < 8; ++wd) m += __popc(rt.mask[wd]); rt.m = m; }
     __syncthreads();
+}
+
+// route() from sel / rw in LDS or global memory (generic loads)
+__device__ void route(const int64_t* sel, const uint16_t* rw, int R, int lo, int n_hot, Route& rt)
+{
+    const int i = min((int) threadIdx.x, R * TOPK - 1);
+    route_picks({sel[i], rw[i]}, R, lo, n_hot, rt);
 }
 
 // bf16 group scale k (0..3) of the four packed in s
@@ -114,45 +135,92 @@ __global__ void __launch_bounds__(NT) router_kernel(const uint16_t* __restrict__
     expert_logits(x, wt, 2 * blockIdx.x + half, E, R, H, tid, sums[half], logits);
 }
 
-// ---- routed gate/up ----
+// ---- gate/up: the shared expert's unit first (it needs no routing), then the routed items ----
 struct GuItem
 {
     u32x4 g[4], u[4];                       // the wave's 4 k groups of gate and up (one 16-byte load per lane each)
     u32x2 sg, su;                           // their 4 group scales of the lane's row
 };
 
-__global__ void __launch_bounds__(GW * 64) gu5_kernel(
+constexpr int GU_SH_GRID = 2 * NB_I;        // with the shared expert: workgroup b owns matrix b & 1 of row block b >> 1
+
+// SH: workgroup b first computes the full-K sum of one shared matrix (gate for even b, up for odd b) over 16 rows of I
+// as two 8-tile units (wave w: k steps 16 w + 8 j .. + 8 of F16T, against its own x fragments), loaded before the
+// routing prologue so that their loads cover it; the wave-ordered fp32 sums go to the SHP_SLOT area of act, and the
+// down launch forms the shared act f16(silu(g) u) from them. Then the routed items b, b + G, ... (slot, 16-row block).
+template <bool SH>
+__global__ void __launch_bounds__(GW * 64) gu7_kernel(
     const void* __restrict__ x, int xf, const float* __restrict__ logits, const float* __restrict__ bias, int E,
     int topk, float scale, int64_t* __restrict__ sel, uint16_t* __restrict__ rw, int R, int lo, int n_hot,
     const int64_t* __restrict__ gate_w, const int64_t* __restrict__ up_w, const int64_t* __restrict__ gate_s,
-    const int64_t* __restrict__ up_s, _Float16* __restrict__ act)
+    const int64_t* __restrict__ up_s, const uint8_t* __restrict__ sh_gw, const uint8_t* __restrict__ sh_uw,
+    _Float16* __restrict__ act)
 {
     __shared__ Route rt;
+    __shared__ const uint8_t* tab[4][HMOE_MAXE];
     __shared__ const uint8_t* ptr[4][MAXSLOT];
     __shared__ int64_t ssel[MAXR * TOPK];
     __shared__ uint16_t srw[MAXR * TOPK];
     __shared__ f32x4 red[2][GW][2][64];
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, tok = l & 15, ks = l >> 4;
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, tok = l & 15, ks = l >> 4, row = l & 15;
+    const int b = blockIdx.x, G = gridDim.x;
     const bool live = tok < R;
+    // Loads are issued in the order they are consumed (the wait counter is in order) and unconditionally (a load
+    // under a branch makes the compiler wait for every outstanding load where the paths meet): x, the window's
+    // pointer tables (x standing in without a window), the logits of the wave's rows, then the shared units.
+    const uint16_t* xr = (const uint16_t*) x + (size_t) (live ? tok : 0) * H + 512 * w + 8 * ks;
+    u32x4 raw[16];
+    #pragma unroll
+    for (int t = 0; t < 16; ++t) raw[t] = ld16(xr + 32 * t);
+    const int te = min((int) threadIdx.x, max(n_hot - 1, 0));
+    const bool hot = n_hot > 0;
+    const int64_t* xt = (const int64_t*) x;
+    const int64_t t0 = ldg<int64_t>(hot ? gate_w + te : xt), t1 = ldg<int64_t>(hot ? up_w + te : xt);
+    const int64_t t2 = ldg<int64_t>(hot ? gate_s + te : xt), t3 = ldg<int64_t>(hot ? up_s + te : xt);
+    RowIn r0, r1;                                              // rows w and w + GW (one bias)
+    if (logits)
+    {
+        load_logits_global(logits + (size_t) min(w, R - 1) * RMAXE, E, r0.lg);
+        load_logits_global(logits + (size_t) min(w + GW, R - 1) * RMAXE, E, r1.lg);
+        load_bias_global(bias, logits, E, r0.b);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the first shared unit goes out before the routing prologue (the second right after it: both at once would
+    // not fit the registers next to x)
+    GuItem A, B;
+    const uint8_t* shm = (b & 1) ? sh_uw : sh_gw;
+    const uint8_t* shbase = shm + ((size_t) ((b >> 1) * KS_H + 16 * w) * 64 + l) * 16;
+    if (SH)
+    {
+        #pragma unroll
+        for (int q = 0; q < 4; ++q)
+        {
+            A.g[q] = ldw16(shbase + q * 1024); A.u[q] = ldw16(shbase + (4 + q) * 1024);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
     // the rows' x for this wave's k range: k step t covers k = 512 w + 32 t + 8 ks .. + 8 of row tok (A operand)
     f16x8 xa[16];
     {
-        const uint16_t* xr = (const uint16_t*) x + (size_t) (live ? tok : 0) * H + 512 * w + 8 * ks;
+        const uint32_t lm = live ? 0xffffffffu : 0u;
         #pragma unroll
         for (int t = 0; t < 16; ++t)
         {
-            const u32x4 v = ld16(xr + 32 * t);
-            xa[t] = live ? (xf ? as_f16x8(v) : bf8_to_f16(v)) : (f16x8) {};
+            const u32x4 v = raw[t] & lm;
+            xa[t] = xf ? as_f16x8(v) : bf8_to_f16(v);
         }
     }
+    // every thread stores (threads past n_hot repeat entry n_hot - 1 with its own value)
+    tab[0][te] = (const uint8_t*) t0; tab[1][te] = (const uint8_t*) t1;
+    tab[2][te] = (const uint8_t*) t2; tab[3][te] = (const uint8_t*) t3;
     if (logits)
     {
-        if (w < R) select_row(logits + (size_t) w * RMAXE, bias, E, topk, scale, ssel + w * TOPK, srw + w * TOPK);
-        if (w + GW < R)
-            select_row(logits + (size_t) (w + GW) * RMAXE, bias, E, topk, scale, ssel + (w + GW) * TOPK,
-                       srw + (w + GW) * TOPK);
+        if (w < R) select_from(r0, E, topk, scale, ssel + w * TOPK, srw + w * TOPK);
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) r1.b[i] = r0.b[i];
+        if (w + GW < R) select_from(r1, E, topk, scale, ssel + (w + GW) * TOPK, srw + (w + GW) * TOPK);
         __syncthreads();
-        if (blockIdx.x == 0 && threadIdx.x < R * TOPK) { sel[threadIdx.x] = ssel[threadIdx.x]; rw[threadIdx.x] = srw[threadIdx.x]; }
+        if (b == 0 && threadIdx.x < R * TOPK) { sel[threadIdx.x] = ssel[threadIdx.x]; rw[threadIdx.x] = srw[threadIdx.x]; }
         route(ssel, srw, R, lo, n_hot, rt);
     }
     else route(sel, rw, R, lo, n_hot, rt);
@@ -160,29 +228,34 @@ __global__ void __launch_bounds__(GW * 64) gu5_kernel(
     if (threadIdx.x < m)
     {
         const int e = rt.e[threadIdx.x];
-        ptr[0][threadIdx.x] = (const uint8_t*) gate_w[e]; ptr[1][threadIdx.x] = (const uint8_t*) up_w[e];
-        ptr[2][threadIdx.x] = (const uint8_t*) gate_s[e]; ptr[3][threadIdx.x] = (const uint8_t*) up_s[e];
+        ptr[0][threadIdx.x] = tab[0][e]; ptr[1][threadIdx.x] = tab[1][e];
+        ptr[2][threadIdx.x] = tab[2][e]; ptr[3][threadIdx.x] = tab[3][e];
     }
+    // no routed expert: slot 0 stands in as the shared matrix (25 MB, beyond every offset a stand-in load reaches)
+    if (m == 0 && threadIdx.x < 4) ptr[threadIdx.x][0] = shm;
     __syncthreads();
-    const int G = gridDim.x, total = m * NB_I;
-    const int nmine = (int) blockIdx.x < total ? (total - 1 - (int) blockIdx.x) / G + 1 : 0;
-    if (nmine == 0) return;                                    // uniform over the workgroup
-    const int row = l & 15;
+    const int total = m * NB_I;
+    const int nr = b < total ? (total - 1 - b) / G + 1 : 0;
+    if (!SH && nr == 0) return;                                // uniform over the workgroup
     const DqConsts dq = dq_consts();
+    // routed item i < nr; past the end (the ring's last prefetch, or no routed item at all) the four loads of a
+    // matrix all read one tile (k stride 0): 1 KB instead of repeating the item's 4 KB (an integer select: a pointer
+    // select here becomes a branch whose register copies wait for every load in flight)
     auto load = [&](GuItem& S, int i) {
-        const int it = blockIdx.x + i * G, j = it / NB_I, nb = it - j * NB_I;
+        const int it = b + min(i, max(nr - 1, 0)) * G, j = min(it / NB_I, max(m - 1, 0)), nb = it - (it / NB_I) * NB_I;
         const size_t toff = ((size_t) (nb * KG_H + 4 * w) * 64 + l) * 16;
         const size_t soff = ((size_t) (nb * 16 + row) * KG_H + 4 * w) * 2;
+        const int kst = i < nr ? 1024 : 0;
         #pragma unroll
         for (int k = 0; k < 4; ++k)
         {
-            S.g[k] = ldw16(ptr[0][j] + toff + k * 1024);
-            S.u[k] = ldw16(ptr[1][j] + toff + k * 1024);
+            S.g[k] = ldw16(ptr[0][j] + toff + k * kst);
+            S.u[k] = ldw16(ptr[1][j] + toff + k * kst);
         }
         S.sg = ld8(ptr[2][j] + soff); S.su = ld8(ptr[3][j] + soff);
     };
     auto run = [&](const GuItem& S, int i, int par) {
-        const int it = blockIdx.x + i * G, j = it / NB_I, nb = it - j * NB_I;
+        const int it = b + i * G, j = it / NB_I, nb = it - j * NB_I;
         f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
         #pragma unroll
         for (int k = 0; k < 4; ++k)
@@ -205,66 +278,200 @@ __global__ void __launch_bounds__(GW * 64) gu5_kernel(
         }
         // red[par] is written again two items later, after the next item's barrier: no second barrier needed
     };
-    GuItem A, B;
-    load(A, 0);
-    for (int i = 0; i < nmine; i += 2)
+    if (SH)
     {
-        load(B, min(i + 1, nmine - 1));
+        // the shared units (A: k steps 16 w .. + 8, B: + 8 .. + 16) interleaved with the first routed prefetches
+        #pragma unroll
+        for (int q = 0; q < 4; ++q)
+        {
+            B.g[q] = ldw16(shbase + (8 + q) * 1024); B.u[q] = ldw16(shbase + (12 + q) * 1024);
+        }
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) acc = mfma16(xa[q], as_f16x8(A.g[q]), acc);
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) acc = mfma16(xa[4 + q], as_f16x8(A.u[q]), acc);
+        load(A, 0);
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) acc = mfma16(xa[8 + q], as_f16x8(B.g[q]), acc);
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) acc = mfma16(xa[12 + q], as_f16x8(B.u[q]), acc);
+        // wave-ordered sum through red[1] (routed item 0 writes red[0] next; item 1 writes red[1] after item 0's
+        // barrier, which every reader here has passed)
+        red[1][w][0][l] = acc;
+        __syncthreads();
+        if (threadIdx.x < 256)
+        {
+            const int ll = threadIdx.x >> 2, ie = threadIdx.x & 3, tk = 4 * (ll >> 4) + ie;
+            if (tk < R)
+            {
+                float sum = 0.f;
+                #pragma unroll
+                for (int ww = 0; ww < GW; ++ww) sum += red[1][ww][0][ll][ie];
+                float* shp = (float*) (act + (size_t) SHP_SLOT * MAXR * I);
+                shp[((size_t) (b & 1) * MAXR + tk) * I + (b >> 1) * 16 + (ll & 15)] = sum;
+            }
+        }
+    }
+    else load(A, 0);
+    // A holds routed item 0 (or a stand-in)
+    for (int i = 0; i < nr; i += 2)
+    {
+        load(B, i + 1);
         run(A, i, 0);
-        if (i + 1 >= nmine) break;
-        load(A, min(i + 2, nmine - 1));
+        if (i + 1 >= nr) break;
+        load(A, i + 2);
         run(B, i + 1, 1);
     }
 }
 
-// ---- routed down ----
+// ---- down: the shared expert's items first (they need no routing), then the routed (slot quad, row block) items ----
 struct DnItem
 {
-    u32x4 d[4];                             // the wave's 4 k groups of one 16-row block of down
-    u32x2 s;                                // their 4 group scales of the lane's row
+    u32x4 d[4];                             // the wave's 4 tiles of one 16-row block of down
+    u32x2 s;                                // their 4 group scales of the lane's row (routed items)
 };
 
-__global__ void __launch_bounds__(DW * 64) dn5_kernel(
+constexpr int DN_GMIN = NB_H / 2, DN_GMAX = NB_H;   // grid range: one or two shared items per workgroup
+
+// workgroup b: (SH) shared items nb = b and b + G (when < NB_H), then a contiguous range of the routed items
+// (quad-major, so a quad's act stays in registers). Every item moves the same 64 KB; the ranges give every workgroup
+// floor or ceil of (shared + routed) / G items in total. The shared act, f16(silu(g) u), is formed here from the fp32
+// gate and up sums the gate/up launch left in the SHP_SLOT area of act.
+template <bool SH>
+__global__ void __launch_bounds__(DW * 64) dn6_kernel(
     const int64_t* __restrict__ sel, const uint16_t* __restrict__ rw, int R, int lo, int n_hot,
     const int64_t* __restrict__ down_w, const int64_t* __restrict__ down_s, const _Float16* __restrict__ act,
-    float* __restrict__ y32, int* __restrict__ nparts_out, int part0)
+    const uint8_t* __restrict__ sh_dw, float* __restrict__ y32, int* __restrict__ nparts_out)
 {
     __shared__ Route rt;
+    __shared__ const uint8_t* tab[2][HMOE_MAXE];
     __shared__ const uint8_t* ptr[2][MAXSLOT];
     __shared__ f32x4 red[2][DW][64];
-    route(sel, rw, R, lo, n_hot, rt);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, tok = l & 15, ks = l >> 4, row = l & 15;
+    const int sw = w >> 2, kq = w & 3;                          // routed items: slot of the quad, k quarter of I
+    const bool live = tok < R;
+    const int G = gridDim.x, b = blockIdx.x;
+    const int part0 = SH ? 1 : 0, nsh = SH ? NB_H : 0;
+    const int s_mine = SH ? (b + G < NB_H ? 2 : 1) : 0;       // (G <= NB_H: every workgroup has one)
+    // loads in issue order: pointer tables, picks, the shared act, the shared items (all independent of routing)
+    // (every load here is unconditional, with a valid stand-in address where there is nothing to load: a load under a
+    // branch makes the compiler wait for all outstanding loads where the paths meet)
+    const int te = min((int) threadIdx.x, max(n_hot - 1, 0));
+    const int64_t t0 = ldg<int64_t>(n_hot > 0 ? down_w + te : sel), t1 = ldg<int64_t>(n_hot > 0 ? down_s + te : sel);
+    const Pick pk = load_pick_global(sel, rw, R);
+    __builtin_amdgcn_sched_barrier(0);                          // keep the routing loads ahead of the item loads
+    // shared items: wave w owns k group w of I (4 k steps of F16T) with the shared act of its k group as the A operand,
+    // formed from the fp32 sums (loaded first, so forming it does not wait for the tiles); the second item is the
+    // first one again when there is none (an L2 hit)
+    f16x8 xs[4];
+    u32x4 S0[4], S1[4];
+    if (SH)
+    {
+        const float* shp = (const float*) (act + (size_t) SHP_SLOT * MAXR * I) + (size_t) (live ? tok : 0) * I + 128 * w + 8 * ks;
+        u32x4 gv[8], uv[8];
+        #pragma unroll
+        for (int t = 0; t < 4; ++t)
+        {
+            gv[2 * t] = ld16(shp + 32 * t); gv[2 * t + 1] = ld16(shp + 32 * t + 4);
+            uv[2 * t] = ld16(shp + MAXR * I + 32 * t); uv[2 * t + 1] = ld16(shp + MAXR * I + 32 * t + 4);
+        }
+        const uint8_t* w0 = sh_dw + ((size_t) (b * KS_I + 4 * w) * 64 + l) * 16;
+        const uint8_t* w1 = sh_dw + ((size_t) ((s_mine == 2 ? b + G : b) * KS_I + 4 * w) * 64 + l) * 16;
+        #pragma unroll
+        for (int k = 0; k < 4; ++k) S0[k] = ldw16(w0 + k * 1024);
+        #pragma unroll
+        for (int k = 0; k < 4; ++k) S1[k] = ldw16(w1 + k * 1024);
+        __builtin_amdgcn_sched_barrier(0);
+        #pragma unroll
+        for (int t = 0; t < 4; ++t)
+        {
+            f16x8 v;
+            #pragma unroll
+            for (int e = 0; e < 8; ++e)
+            {
+                const float g = __uint_as_float(gv[2 * t + (e >> 2)][e & 3]), u = __uint_as_float(uv[2 * t + (e >> 2)][e & 3]);
+                v[e] = (_Float16) (silu(g) * u);
+            }
+            xs[t] = live ? v : (f16x8) {};
+        }
+    }
+    // every thread stores (threads past n_hot repeat entry n_hot - 1 with its own value): a store under a branch
+    // would pull the table loads into it, behind the item loads
+    tab[0][te] = (const uint8_t*) t0; tab[1][te] = (const uint8_t*) t1;
+    route_picks(pk, R, lo, n_hot, rt);
     const int m = rt.m, nq = (m + 3) / 4;
     if (threadIdx.x < m)
     {
         const int e = rt.e[threadIdx.x];
-        ptr[0][threadIdx.x] = (const uint8_t*) down_w[e]; ptr[1][threadIdx.x] = (const uint8_t*) down_s[e];
+        ptr[0][threadIdx.x] = tab[0][e]; ptr[1][threadIdx.x] = tab[1][e];
     }
-    if (blockIdx.x == 0 && threadIdx.x == 0) *nparts_out = part0 + nq;
+    // no routed expert: slot 0 stands in as act, so the first routed load below stays unconditional and in bounds
+    if (m == 0 && threadIdx.x == 0) { ptr[0][0] = (const uint8_t*) act; ptr[1][0] = (const uint8_t*) act; }
+    if (b == 0 && threadIdx.x == 0) *nparts_out = part0 + nq;
     __syncthreads();
-    // items (quad, nb), quad-major, a contiguous range per workgroup (the act of a quad stays in registers)
-    const int G = gridDim.x, total = nq * NB_H;
-    const int i0 = (int) (((long long) total * blockIdx.x) / G), i1 = (int) (((long long) total * (blockIdx.x + 1)) / G);
-    const int nmine = i1 - i0;
-    if (nmine <= 0) return;                                    // uniform over the workgroup
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, tok = l & 15, ks = l >> 4, row = l & 15;
-    const int sw = w >> 2, kq = w & 3;                          // slot of the quad, k quarter of I
-    const bool live = tok < R;
-    f16x8 xa[16];
-    int cur_q = -1;
+    int r0, nr;
+    {
+        const long long rt_n = (long long) nq * NB_H, T = nsh + rt_n;
+        auto start = [&](int bb) {                              // routed items before workgroup bb
+            const long long sh_before = (long long) (nsh / G) * bb + min(bb, nsh % G);
+            return (int) max(0ll, min(rt_n, T * bb / G - sh_before));
+        };
+        r0 = start(b);
+        nr = max(0, start(b + 1) - r0);
+    }
+    if (s_mine + nr == 0) return;                              // uniform over the workgroup
     const DqConsts dq = dq_consts();
+    // routed item i; a slot past m reads one fixed tile of slot m - 1 with the same loads (no HBM traffic), and past
+    // the end (the ring's last prefetch) the four loads read the last item's first tile (k stride 0: 1 KB, not 4 KB)
     auto load = [&](DnItem& S, int i) {
-        const int it = i0 + i, qd = it / NB_H, nb = it - qd * NB_H, j = 4 * qd + sw;
-        // a slot past m loads one fixed tile of slot m - 1 (the same load count on every path, no HBM traffic)
+        const int it = r0 + min(i, max(nr - 1, 0)), qd = it / NB_H, nb = it - qd * NB_H, j = 4 * qd + sw;
         const bool ok = j < m;
-        const int jj = ok ? j : m - 1, nbb = ok ? nb : 0;
+        const int jj = max(min(j, m - 1), 0), nbb = ok ? nb : 0;
         const size_t toff = ((size_t) (nbb * KG_I + 4 * kq) * 64 + l) * 16;
         const size_t soff = ((size_t) (nbb * 16 + row) * KG_I + 4 * kq) * 2;
+        const int kst = (ok && i < nr) ? 1024 : 0;
         #pragma unroll
-        for (int k = 0; k < 4; ++k) S.d[k] = ldw16(ptr[0][jj] + toff + (ok ? k * 1024 : 0));
+        for (int k = 0; k < 4; ++k) S.d[k] = ldw16(ptr[0][jj] + toff + k * kst);
         S.s = ld8(ptr[1][jj] + soff);
     };
+    // the sum of the 16 wave partials of a 16-row block in wave order -> y32[part]
+    auto reduce = [&](const f32x4& acc, int par, int part, int nb) {
+        red[par][w][l] = acc;
+        __syncthreads();
+        if (threadIdx.x < 256)
+        {
+            const int ll = threadIdx.x >> 2, ie = threadIdx.x & 3, tk = 4 * (ll >> 4) + ie;
+            if (tk < R)
+            {
+                float sum = 0.f;
+                #pragma unroll
+                for (int ww = 0; ww < DW; ++ww) sum += red[par][ww][ll][ie];
+                y32[((size_t) part * MAXR + tk) * H + nb * 16 + (ll & 15)] = sum;
+            }
+        }
+        // red[par] is written again two items later, after the next item's barrier
+    };
+    DnItem A, B;
+    load(A, 0);                                                 // (unconditional: a stand-in tile when nr == 0)
+    if (SH)
+    {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        #pragma unroll
+        for (int t = 0; t < 4; ++t) acc = mfma16(xs[t], as_f16x8(S0[t]), acc);
+        reduce(acc, 0, 0, b);
+        if (s_mine == 2)
+        {
+            acc = (f32x4) {0.f, 0.f, 0.f, 0.f};
+            #pragma unroll
+            for (int t = 0; t < 4; ++t) acc = mfma16(xs[t], as_f16x8(S1[t]), acc);
+            reduce(acc, 1, 0, b + G);
+        }
+    }
+    int cur_q = -1;
+    f16x8 xa[16];
     auto run = [&](const DnItem& S, int i, int par) {
-        const int it = i0 + i, qd = it / NB_H, nb = it - qd * NB_H;
+        const int it = r0 + i, qd = it / NB_H, nb = it - qd * NB_H;
         if (qd != cur_q)
         {
             // the quad's act rows for this wave's slot and k quarter (zero for a slot past m)
@@ -282,120 +489,17 @@ __global__ void __launch_bounds__(DW * 64) dn5_kernel(
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         #pragma unroll
         for (int k = 0; k < 4; ++k) group_i4(xa + 4 * k, S.d[k], scale_of(S.s, k), acc, dq);
-        red[par][w][l] = acc;
-        __syncthreads();
-        if (threadIdx.x < 256)
-        {
-            const int ll = threadIdx.x >> 2, ie = threadIdx.x & 3, tk = 4 * (ll >> 4) + ie;
-            if (tk < R)
-            {
-                float s = 0.f;
-                #pragma unroll
-                for (int ww = 0; ww < DW; ++ww) s += red[par][ww][ll][ie];
-                y32[((size_t) (part0 + qd) * MAXR + tk) * H + nb * 16 + (ll & 15)] = s;
-            }
-        }
+        reduce(acc, par, part0 + qd, nb);
     };
-    DnItem A, B;
-    load(A, 0);
-    for (int i = 0; i < nmine; i += 2)
+    const int p0 = s_mine & 1;                                  // red parity of the first routed item
+    for (int i = 0; i < nr; i += 2)
     {
-        load(B, min(i + 1, nmine - 1));
-        run(A, i, 0);
-        if (i + 1 >= nmine) break;
-        load(A, min(i + 2, nmine - 1));
-        run(B, i + 1, 1);
+        load(B, i + 1);
+        run(A, i, p0);
+        if (i + 1 >= nr) break;
+        load(A, i + 2);
+        run(B, i + 1, p0 ^ 1);
     }
-}
-
-// the 8 wave partials of a 16-row block, summed in wave order: thread t < 256 gets (row t/16, token t%16) of the
-// standard MFMA output layout (lane l: rows 4(l/16)..+4, column l%16)
-__device__ __forceinline__ float wave_sum(const float (*red)[64][8], int comp)
-{
-    const int row = threadIdx.x >> 4, tk = threadIdx.x & 15;
-    const int ll = (row >> 2) * 16 + tk, ie = row & 3;
-    float s = 0.f;
-    #pragma unroll
-    for (int w = 0; w < NW; ++w) s += red[w][ll][comp + ie];
-    return s;
-}
-
-// ---- shared gate/up (F16T, full K per item nb): 8 waves on 8 k ranges, act[SH_SLOT] = f16(silu(g) u) ----
-template <int D>
-__global__ void __launch_bounds__(512) sh_gu_kernel(const void* __restrict__ x, int xf, int R,
-                                                    const uint8_t* __restrict__ gw, const uint8_t* __restrict__ uw,
-                                                    _Float16* __restrict__ act)
-{
-    constexpr int KW = KS_H / 8;                                       // 24 k steps per wave
-    static_assert(KW % D == 0, "the ring depth divides the k steps of a wave");
-    __shared__ float red[8][64][8];
-    const int nb = blockIdx.x, w = threadIdx.x >> 6, l = threadIdx.x & 63, tok = l & 15, ks = l >> 4;
-    const bool live = tok < R;
-    const size_t xo = (size_t) (live ? tok : 0) * H + 8 * ks;
-    const size_t off0 = ((size_t) (nb * KS_H + w * KW) * 64 + l) * 16;
-    u32x4 gq[D], uq[D], xq[D];
-    auto issue = [&](int q, auto sc) {
-        constexpr int s = decltype(sc)::value;
-        gq[s] = ldw16(gw + off0 + (size_t) q * 1024); uq[s] = ldw16(uw + off0 + (size_t) q * 1024);
-        xq[s] = ld16((const uint16_t*) x + xo + (size_t) (w * KW + q) * 32);   // bf16 or f16: 8 elements
-    };
-    f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
-    static_for<D>([&](auto sc) { issue(decltype(sc)::value, sc); });
-    for (int q0 = 0; q0 < KW; q0 += D)
-        static_for<D>([&](auto sc) {
-            constexpr int s = decltype(sc)::value;
-            f16x8 bv = {};
-            if (live) bv = xf ? as_f16x8(xq[s]) : bf8_to_f16(xq[s]);
-            ag = mfma16(as_f16x8(gq[s]), bv, ag);
-            au = mfma16(as_f16x8(uq[s]), bv, au);
-            if (q0 + s + D < KW) issue(q0 + s + D, sc);
-        });
-    #pragma unroll
-    for (int i = 0; i < 4; ++i) { red[w][l][i] = ag[i]; red[w][l][4 + i] = au[i]; }
-    __syncthreads();
-    if (threadIdx.x < 256)
-    {
-        const int row = threadIdx.x >> 4, tk = threadIdx.x & 15;
-        if (tk < R)
-        {
-            const float g = wave_sum(red, 0), u = wave_sum(red, 4);
-            act[((size_t) SH_SLOT * MAXR + tk) * I + nb * 16 + row] = (_Float16) (silu(g) * u);
-        }
-    }
-}
-
-// ---- shared down (F16T, item nb of H): 4 waves on 4 k ranges of I -> y32[0] ----
-template <int D>
-__global__ void __launch_bounds__(256) sh_dn_kernel(int R, const uint8_t* __restrict__ dw,
-                                                    const _Float16* __restrict__ act, float* __restrict__ y32)
-{
-    constexpr int KW = KS_I / 4;                                       // 16 k steps per wave
-    static_assert(KW % D == 0, "the ring depth divides the k steps of a wave");
-    __shared__ f32x4 red[4][64];
-    const int nb = blockIdx.x, w = threadIdx.x >> 6, l = threadIdx.x & 63, tok = l & 15, ks = l >> 4;
-    const bool live = tok < R;
-    const _Float16* arow = act + ((size_t) SH_SLOT * MAXR + (live ? tok : 0)) * I + 8 * ks + w * KW * 32;
-    const size_t off0 = ((size_t) (nb * KS_I + w * KW) * 64 + l) * 16;
-    u32x4 dq[D], xq[D];
-    auto issue = [&](int q, auto sc) {
-        constexpr int s = decltype(sc)::value;
-        dq[s] = ldw16(dw + off0 + (size_t) q * 1024);
-        xq[s] = ld16(arow + q * 32);
-    };
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    static_for<D>([&](auto sc) { issue(decltype(sc)::value, sc); });
-    for (int q0 = 0; q0 < KW; q0 += D)
-        static_for<D>([&](auto sc) {
-            constexpr int s = decltype(sc)::value;
-            acc = mfma16(as_f16x8(dq[s]), live ? as_f16x8(xq[s]) : (f16x8) {}, acc);
-            if (q0 + s + D < KW) issue(q0 + s + D, sc);
-        });
-    red[w][l] = acc;
-    __syncthreads();
-    const int row = threadIdx.x >> 4, tk = threadIdx.x & 15;
-    const int ll = (row >> 2) * 16 + tk, ie = row & 3;
-    if (tk < R)
-        y32[(size_t) tk * H + nb * 16 + row] = ((red[0][ll][ie] + red[1][ll][ie]) + red[2][ll][ie]) + red[3][ll][ie];
 }
 
 // ---- y (+)= sum of the parts in order; or the layer's bf16 output ----
@@ -455,81 +559,41 @@ static int check(const DecodeArgs& a)
     return HMOE_OK;
 }
 
-// the per-device side stream of the shared expert, joined back before the output reduction
-struct SideStream
-{
-    hipStream_t s = nullptr;
-    hipEvent_t fork = nullptr, join = nullptr;
-};
-
-static int side_stream(SideStream*& out)
-{
-    static SideStream ss[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return set_error(HMOE_ERR_HIP, "side stream: device");
-    SideStream& d = ss[dev];
-    if (!d.s)
-    {
-        if (hipStreamCreateWithFlags(&d.s, hipStreamNonBlocking) != hipSuccess ||
-            hipEventCreateWithFlags(&d.fork, hipEventDisableTiming) != hipSuccess ||
-            hipEventCreateWithFlags(&d.join, hipEventDisableTiming) != hipSuccess)
-            return set_error(HMOE_ERR_HIP, "side stream: create");
-    }
-    out = &d;
-    return HMOE_OK;
-}
-
-// launches; phase mask bit 0 = router logits (+ the shared gate/up on the side stream), 1 = routed gate/up,
-// 2 = routed down (+ the shared down on the side stream), 3 = ordered reduction. blocks: grid of the routed
-// gate/up and down kernels (0 = one workgroup per CU).
+// launches; phase mask bit 0 = router logits, 1 = shared + routed gate/up, 2 = shared + routed down, 3 = ordered
+// reduction. blocks: grid of the gate/up and down kernels (0 = one workgroup per CU); with the shared expert the
+// gate/up grid is GU_SH_GRID (one shared matrix slice each) and the down grid is kept in [DN_GMIN, DN_GMAX].
 static int run_decode(const DecodeArgs& a, int phases, hipStream_t st)
 {
     const int R = a.R;
     const bool sh = a.sh_gw != nullptr;
-    SideStream* ss = nullptr;
-    if (sh)
-    {
-        const int rc = side_stream(ss);
-        if (rc) return rc;
-    }
-    bool forked = false;
-    auto fork = [&]() -> int {
-        if (forked) return HMOE_OK;
-        if (hipEventRecord(ss->fork, st) != hipSuccess || hipStreamWaitEvent(ss->s, ss->fork, 0) != hipSuccess)
-            return set_error(HMOE_ERR_HIP, "moe4: fork");
-        forked = true;
-        return HMOE_OK;
-    };
     const int G = a.blocks ? a.blocks : default_grid(1);
-    if (phases & 1)
-    {
-        if (sh)
-        {
-            if (fork()) return HMOE_ERR_HIP;
-            sh_gu_kernel<6><<<NB_I, 512, 0, ss->s>>>(a.x, a.xf, R, (const uint8_t*) a.sh_gw, (const uint8_t*) a.sh_uw,
-                                                     a.act);
-        }
-        if (a.logits) router_kernel<<<(a.E + 1) / 2, NT, 0, st>>>((const uint16_t*) a.x, R, a.wt, a.E, a.logits);
-    }
+    if ((phases & 1) && a.logits)
+        router_kernel<<<(a.E + 1) / 2, NT, 0, st>>>((const uint16_t*) a.x, R, a.wt, a.E, a.logits);
     const int64_t* sel = a.logits ? a.sel_out : a.sel_in;
     const uint16_t* rw = a.logits ? a.rw_out : a.rw_in;
     if (phases & 2)
-        gu5_kernel<<<G, GW * 64, 0, st>>>(a.x, a.xf, a.logits, a.bias, a.E, a.topk, a.scale,
-                                          a.logits ? a.sel_out : (int64_t*) a.sel_in,
-                                          a.logits ? a.rw_out : (uint16_t*) a.rw_in, R, a.lo, a.n_hot, a.gate_w,
-                                          a.up_w, a.gate_s, a.up_s, a.act);
+    {
+        int64_t* so = a.logits ? a.sel_out : (int64_t*) a.sel_in;
+        uint16_t* ro = a.logits ? a.rw_out : (uint16_t*) a.rw_in;
+        if (sh)
+            gu7_kernel<true><<<GU_SH_GRID, GW * 64, 0, st>>>(a.x, a.xf, a.logits, a.bias, a.E, a.topk, a.scale, so, ro, R,
+                                                             a.lo, a.n_hot, a.gate_w, a.up_w, a.gate_s, a.up_s,
+                                                             (const uint8_t*) a.sh_gw, (const uint8_t*) a.sh_uw, a.act);
+        else
+            gu7_kernel<false><<<G, GW * 64, 0, st>>>(a.x, a.xf, a.logits, a.bias, a.E, a.topk, a.scale, so, ro, R,
+                                                     a.lo, a.n_hot, a.gate_w, a.up_w, a.gate_s, a.up_s, nullptr,
+                                                     nullptr, a.act);
+    }
     if (phases & 4)
     {
+        const int gd = min(max(G, DN_GMIN), DN_GMAX);
         if (sh)
-        {
-            if (fork()) return HMOE_ERR_HIP;
-            sh_dn_kernel<8><<<NB_H, 256, 0, ss->s>>>(R, (const uint8_t*) a.sh_dw, a.act, a.y32);
-        }
-        dn5_kernel<<<G, DW * 64, 0, st>>>(sel, rw, R, a.lo, a.n_hot, a.down_w, a.down_s, a.act, a.y32, a.ctr,
-                                          sh ? 1 : 0);
+            dn6_kernel<true><<<gd, DW * 64, 0, st>>>(sel, rw, R, a.lo, a.n_hot, a.down_w, a.down_s, a.act,
+                                                     (const uint8_t*) a.sh_dw, a.y32, a.ctr);
+        else
+            dn6_kernel<false><<<gd, DW * 64, 0, st>>>(sel, rw, R, a.lo, a.n_hot, a.down_w, a.down_s, a.act, nullptr,
+                                                      a.y32, a.ctr);
     }
-    if (forked && (hipEventRecord(ss->join, ss->s) != hipSuccess || hipStreamWaitEvent(st, ss->join, 0) != hipSuccess))
-        return set_error(HMOE_ERR_HIP, "moe4: join");
     if (phases & 8) dec_d_kernel<<<(R * H / 4 + 255) / 256, 256, 0, st>>>(a.y32, a.ctr, R, a.y, a.out);
     return HMOE_LAUNCHED("moe4");
 }
@@ -542,7 +606,7 @@ extern "C" size_t hmoe_moe4_scratch_bytes(int which)
 {
     switch (which)
     {
-        case 0: return (size_t) ACT_SLOTS * MAXR * I * 2;               // act f16 [132][16][2048]
+        case 0: return (size_t) ACT_SLOTS * MAXR * I * 2;               // act f16 [133][16][2048]
         case 1: return 256;                                             // gu32 (unused: kept for the argument)
         case 2: return (size_t) CTR_WORDS * 4;                          // ctr_a: the part count
         case 3: return (size_t) MAX_PARTS * MAXR * H * 4;               // y32: down part partials

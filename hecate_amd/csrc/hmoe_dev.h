@@ -17,7 +17,8 @@ namespace hmoe {
 
 constexpr int H = HMOE_H, I = HMOE_I, TOPK = HMOE_TOPK, MAXR = HMOE_MAXR, MAXSLOT = HMOE_MAXSLOT;
 constexpr int SH_SLOT = MAXSLOT;            // act slot of the shared expert
-constexpr int ACT_SLOTS = MAXSLOT + 1 + 3;  // + the f16 copy of x ([16][H] = 3 slots of [16][I]) after the shared slot
+constexpr int SHP_SLOT = MAXSLOT + 1;       // the shared expert's fp32 gate and up sums [2][MAXR][I] (4 slots' room)
+constexpr int ACT_SLOTS = MAXSLOT + 1 + 4;
 
 // ---- error state of the C ABI (common.hip) ----
 int set_error(int code, const char* fmt, ...);
@@ -93,7 +94,8 @@ __device__ __forceinline__ f16x8 as_f16x8(u32x4 v) { return __builtin_bit_cast(f
 
 // Loads from global memory through pointers the compiler cannot trace to a kernel argument (expert addresses read from
 // a table): the explicit global address space makes them global_load. A generic pointer would give flat_load, which
-// also counts against the LDS wait counter, so every LDS wait would drain the weight loads in flight.
+// also counts against the LDS wait counter, so every LDS wait would drain the weight loads in flight. The pointer must
+// address global memory: a generic pointer into LDS read this way is an illegal access.
 #define HMOE_GLOBAL __attribute__((address_space(1)))
 template <typename T> __device__ __forceinline__ T ldg(const void* p) { return *(const HMOE_GLOBAL T*) p; }
 // weights read once: nontemporal (not kept in the caches)
@@ -105,8 +107,32 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 
 // top-k of one row by a wave: keys of experts lane + 64 i; each round takes the largest (key, -index) pair, so ties
 // go to the lowest index (exl3_router.py:106-121); the sum runs over the selected unbiased activations in order
-__device__ inline void select_row(const float* __restrict__ lg, const float* __restrict__ bias, int E, int topk, float scale,
-                           int64_t* __restrict__ sel, uint16_t* __restrict__ rw)
+// the inputs of one row's selection held by a lane: logits and bias of experts lane + 64 i (i < 4)
+struct RowIn { float lg[4], b[4]; };
+
+// from global memory, every load unconditional (index clamped to E - 1, the logits standing in for a NULL bias), so
+// a kernel can issue them ahead of other loads and select later: the logits of a row, and the bias
+__device__ __forceinline__ void load_logits_global(const float* __restrict__ lg, int E, float (&out)[4])
+{
+    const int lane = threadIdx.x & 63;
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = ldg<float>(lg + min(lane + 64 * i, E - 1));
+}
+__device__ __forceinline__ void load_bias_global(const float* __restrict__ bias, const float* __restrict__ lg, int E,
+                                                 float (&out)[4])
+{
+    const int lane = threadIdx.x & 63;
+    #pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        const int e = min(lane + 64 * i, E - 1);
+        const float bv = ldg<float>(bias ? bias + e : lg + e);
+        out[i] = bias ? bv : 0.0f;
+    }
+}
+
+__device__ inline void select_from(const RowIn& in, int E, int topk, float scale, int64_t* __restrict__ sel,
+                                   uint16_t* __restrict__ rw)
 {
     const int lane = threadIdx.x & 63;
     float a[4]; uint32_t key[4];
@@ -116,8 +142,8 @@ __device__ inline void select_row(const float* __restrict__ lg, const float* __r
         const int e = lane + 64 * i;
         if (e < E)
         {
-            a[i] = hmoe_sigmoid(lg[e]);
-            key[i] = hmoe_okey(a[i] + (bias ? bias[e] : 0.0f));
+            a[i] = hmoe_sigmoid(in.lg[i]);
+            key[i] = hmoe_okey(a[i] + in.b[i]);
         }
         else { a[i] = 0.f; key[i] = 0u; }
     }
@@ -154,6 +180,22 @@ __device__ inline void select_row(const float* __restrict__ lg, const float* __r
         sel[lane] = isel;
         rw[lane] = hmoe_f2h((wsel * scale) / (sum + 1e-20f));
     }
+}
+
+// select_from on a row in LDS or global memory (generic loads)
+__device__ inline void select_row(const float* __restrict__ lg, const float* __restrict__ bias, int E, int topk,
+                                  float scale, int64_t* __restrict__ sel, uint16_t* __restrict__ rw)
+{
+    const int lane = threadIdx.x & 63;
+    RowIn r;
+    #pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        const int e = lane + 64 * i;
+        r.lg[i] = e < E ? lg[e] : 0.f;
+        r.b[i] = (e < E && bias) ? bias[e] : 0.0f;
+    }
+    select_from(r, E, topk, scale, sel, rw);
 }
 
 

@@ -161,7 +161,8 @@ class MoELayer:
     def decode(self, x, y=None, out=True, with_shared=True, phases=15, blocks=0):
         """the decode layer in four launches (hmoe_moe_decode_layer): router + routed + shared experts of x bf16
         [R, H]; returns the bf16 [R, H] output (out=True) and / or adds into the fp32 y. phases: bit mask of the
-        launches (1 router + shared gate/up, 2 routed gate/up, 4 down, 8 output) for callers that time them apart"""
+        launches (1 router, 2 shared + routed gate/up, 4 shared + routed down, 8 output) for callers that time them
+        apart"""
         R = x.shape[0]
         if not (1 <= R <= 16 and x.dtype == torch.bfloat16 and x.is_contiguous() and x.shape[1] == H):
             raise RuntimeError("decode: x must be contiguous bf16 [R <= 16, 6144]")

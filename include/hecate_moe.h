@@ -81,9 +81,9 @@ int hmoe_router_fused(const void* x, const float* wt, const float* bias, float* 
  * and their scales; y fp32 [R][H] is accumulated into. sh_gw / sh_uw / sh_dw: the shared expert as F16T (gate/up
  * [I][H], down [H][I]) or NULL; sh_gs / sh_us / sh_ds must be NULL (the reference's int8 row scales; F16T has none).
  * Scratch (act, gu32, ctr_a, y32, ctr_b) from hmoe_moe4_scratch_bytes (gu32 and ctr_b unused, kept for the argument
- * positions). blocks: grid size of the routed gate/up and down kernels (0 = one workgroup per CU), blocks_a: unused.
- * The shared expert runs on a per-device side stream forked from and joined back into `stream` (graph-capturable).
- * R in [1, 16]. */
+ * positions). blocks: grid size of the gate/up and down kernels (0 = one workgroup per CU; with the shared expert
+ * the gate/up grid is fixed at 256, and the down grid is kept in [192, 384]), blocks_a: unused. The shared expert
+ * runs inside the routed launches, ahead of the routed items. R in [1, 16]. */
 size_t hmoe_moe4_scratch_bytes(int which);      /* which: 0 act, 1 gu32, 2 ctr_a, 3 y32, 4 ctr_b */
 int hmoe_moe4_forward(const void* x, const int64_t* sel, const uint16_t* rw, int R, int n_hot,
                       const int64_t* gate_w, const int64_t* up_w, const int64_t* down_w,
@@ -92,8 +92,8 @@ int hmoe_moe4_forward(const void* x, const int64_t* sel, const uint16_t* rw, int
                       int lo, const void* sh_gw, const void* sh_uw, const void* sh_dw, const void* sh_gs,
                       const void* sh_us, const void* sh_ds, int xf, void* stream);
 /* the two phases of hmoe_moe4_forward, for callers that time or schedule them apart (this build's addition):
- * gate_up writes act, down adds into y (ctr_b carries its part count); same
- * arguments and rules as forward */
+ * gate_up writes act (with the shared expert: also its fp32 gate and up sums, in act), down adds into y (ctr_b
+ * carries its part count); same arguments and rules as forward */
 int hmoe_moe4_gate_up(const void* x, const int64_t* sel, const uint16_t* rw, int R, int n_hot,
                       const int64_t* gate_w, const int64_t* up_w, const int64_t* gate_s, const int64_t* up_s,
                       void* act, float* gu32, int* ctr_a, int blocks, int lo, const void* sh_gw, const void* sh_uw,
@@ -105,8 +105,8 @@ int hmoe_moe4_down(const int64_t* sel, const uint16_t* rw, int R, int n_hot, con
  * router, the shared expert and moe4 apart): router logits (wt fp32 [E][H], bias) with the router_fused rules, the
  * selection written to sel / rw (int64 / f16 [R][8]), routed experts of the picks in [lo, lo + n_hot) and the shared
  * expert (F16T or NULL); y fp32 [R][H] accumulated into and / or out bf16 [R][H] written (either may be NULL, not
- * both). x bf16 [R][H]. phases: bit mask of the four launches (1 router logits + shared gate/up, 2 routed gate/up,
- * 4 down, 8 output), 15 = the whole layer. topk must be 8. */
+ * both). x bf16 [R][H]. phases: bit mask of the four launches (1 router logits, 2 selection + shared and routed
+ * gate/up, 4 shared and routed down, 8 output), 15 = the whole layer. topk must be 8. */
 int hmoe_moe_decode_layer(const void* x, const float* wt, const float* bias, int E, int topk, float scale,
                           float* logits, int64_t* sel, uint16_t* rw, int R, int n_hot, int lo,
                           const int64_t* gate_w, const int64_t* up_w, const int64_t* down_w,
