@@ -105,8 +105,6 @@ __device__ __forceinline__ u32x2 ld8(const void* p) { return ldg<u32x2>(p); }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
-// top-k of one row by a wave: keys of experts lane + 64 i; each round takes the largest (key, -index) pair, so ties
-// go to the lowest index (exl3_router.py:106-121); the sum runs over the selected unbiased activations in order
 // the inputs of one row's selection held by a lane: logits and bias of experts lane + 64 i (i < 4)
 struct RowIn { float lg[4], b[4]; };
 
@@ -131,6 +129,8 @@ __device__ __forceinline__ void load_bias_global(const float* __restrict__ bias,
     }
 }
 
+// top-k of one row by a wave: keys of experts lane + 64 i; each round takes the largest (key, -index) pair, so ties
+// go to the lowest index (exl3_router.py:106-121); the sum runs over the selected unbiased activations in order
 __device__ inline void select_from(const RowIn& in, int E, int topk, float scale, int64_t* __restrict__ sel,
                                    uint16_t* __restrict__ rw)
 {
