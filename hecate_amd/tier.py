@@ -78,6 +78,40 @@ class ExpertBank:
         return sum(b.numel() for b in self.buf.values())
 
 
+def load_reference_int4(u4dir, layer, experts, device):
+    """The reference's on-disk int4 experts of one layer into an ExpertBank (local id j = experts[j], e.g. a
+    placement's hot prefix): the files u4dir/layer{L}.safetensors and u4dir/layer{L}.r*.safetensors with keys
+    {e}.{gate,up,down}.{q,s} (tier_split.py:207-214; written by tools/quant/gptq_int4.py:205-212): uint8 codes in the
+    moe4 fragment order and fp32 row scales. Each matrix is repacked on the host to I4G128 (hmoe_repack_moe4: the same
+    codes, every group scale = bf16(row scale), a relative change of at most 2^-9)."""
+    import glob
+    import os
+    from safetensors import safe_open
+    files = sorted(glob.glob(os.path.join(u4dir, f"layer{layer}.safetensors")) +
+                   glob.glob(os.path.join(u4dir, f"layer{layer}.r*.safetensors")))
+    if not files:
+        raise RuntimeError(f"load_reference_int4: no layer{layer} files in {u4dir}")
+    handles = [safe_open(f, "np") for f in files]
+    where = {k: h for h in handles for k in h.keys()}
+    bank = ExpertBank(len(experts), device)
+    for j, e in enumerate(experts):
+        for m, (N, K) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
+            kq, ks = f"{e}.{m}.q", f"{e}.{m}.s"
+            if kq not in where or ks not in where:
+                raise RuntimeError(f"load_reference_int4: {kq} / {ks} missing in the layer{layer} files")
+            frag = np.ascontiguousarray(where[kq].get_tensor(kq)).view(np.uint8).reshape(-1)
+            rs = np.ascontiguousarray(where[ks].get_tensor(ks), dtype=np.float32).reshape(-1)
+            if frag.size != N * K // 2 or rs.size != N:
+                raise RuntimeError(f"load_reference_int4: {kq} has {frag.size} bytes and {ks} {rs.size} scales "
+                                   f"(expected {N * K // 2} and {N})")
+            q = np.empty(N * K // 2, np.uint8)
+            sc = np.empty(N * (K // 128), np.uint16)
+            call("hmoe_repack_moe4", frag.ctypes.data, rs.ctypes.data, N, K, q.ctypes.data, sc.ctypes.data)
+            bank.view(f"{m}_q", j).copy_(torch.from_numpy(q))
+            bank.view(f"{m}_s", j).copy_(torch.from_numpy(sc.view(np.uint8)))
+    return bank
+
+
 class PrefillBuffers:
     """device buffers of a prefill chunk of up to T rows: selection, dispatch plan (hmoe_dispatch), GEMM scratch"""
 

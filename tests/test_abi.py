@@ -75,8 +75,7 @@ def test_repack_reference_moe4_weights():
     rng = np.random.default_rng(3)
     N, K = 128, 256
     codes = rng.integers(0, 16, (N, K), dtype=np.uint8)
-    c = codes.reshape(N // 64, 4, 2, 8, K // 64, 4, 2, 4, 2).transpose(0, 4, 1, 3, 7, 5, 8, 6, 2).reshape(-1, 2)
-    frag = (c[:, 0] | (c[:, 1] << 4)).astype(np.uint8)
+    frag = _pack_u4_reference_order(codes)
     rs = (rng.random(N) * 0.01).astype(np.float32)
     q = np.empty(N * K // 2, np.uint8); s = np.empty(N * K // 128, np.uint16)
     _lib.call("hmoe_repack_moe4", frag.ctypes.data, rs.ctypes.data, N, K, q.ctypes.data, s.ctypes.data)
@@ -96,3 +95,43 @@ def test_zipf_tau_is_the_calibrated_one():
     b = synth.zipf_bias()
     order = synth.popularity_order()
     assert np.all(np.diff(b[np.array(order)]) < 0) and sorted(order) == list(range(256))
+
+
+def _pack_u4_reference_order(codes):
+    """tools/quant/gptq_int4.py:74-77 pack_u4, restated as a permutation of the code tensor [N, K] (N % 64 == 0,
+    K % 64 == 0): the bytes the reference writes to its int4 safetensors"""
+    N, K = codes.shape
+    c = codes.reshape(N // 64, 4, 2, 8, K // 64, 4, 2, 4, 2).transpose(0, 4, 1, 3, 7, 5, 8, 6, 2).reshape(-1, 2)
+    return (c[:, 0] | (c[:, 1] << 4)).astype(np.uint8)
+
+
+def test_load_reference_int4_files(tmp_path):
+    """the reference's on-disk layout (hot file + r229 file, keys {e}.{m}.{q,s}, tier_split.py:207-214) read into an
+    ExpertBank in placement order: every matrix's codes exact, group scales = bf16(row scale)"""
+    from safetensors.numpy import save_file
+    from hecate_amd import tier
+    rng = np.random.default_rng(11)
+    H, I = 6144, 2048
+    want = {}
+    hot, cold = {}, {}
+    for e, dst in ((7, hot), (3, cold)):
+        for m, (N, K) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
+            codes = rng.integers(0, 16, (N, K), dtype=np.uint8)
+            rs = (rng.random(N) * 0.01 + 1e-3).astype(np.float32)
+            dst[f"{e}.{m}.q"] = _pack_u4_reference_order(codes)
+            dst[f"{e}.{m}.s"] = rs
+            want[(e, m)] = (codes, rs)
+    save_file(hot, str(tmp_path / "layer5.safetensors"))
+    save_file(cold, str(tmp_path / "layer5.r229.safetensors"))
+    bank = tier.load_reference_int4(str(tmp_path), 5, [3, 7], "cpu")
+    for j, e in enumerate([3, 7]):
+        for m, (N, K) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
+            codes, rs = want[(e, m)]
+            q = bank.view(f"{m}_q", j).numpy().copy()
+            s = bank.view(f"{m}_s", j).numpy().copy().view(np.uint16)
+            c2 = np.empty((N, K // 2), np.uint8); s2 = np.empty((N, K // 128), np.uint16)
+            _lib.call("hmoe_unpack_i4", q.ctypes.data, s.ctypes.data, N, K, c2.ctypes.data, s2.ctypes.data)
+            assert np.array_equal(np.stack([c2 & 15, c2 >> 4], -1).reshape(N, K), codes), (e, m)
+            assert np.array_equal(s2, np.repeat(O.f32_to_bf16(rs)[:, None], K // 128, 1)), (e, m)
+    with pytest.raises(RuntimeError):
+        tier.load_reference_int4(str(tmp_path), 5, [4], "cpu")
