@@ -90,6 +90,15 @@ def test_router_bit_exact(dev, R, bias_sigma):
 # ---- decode ------------------------------------------------------------------------------------------------------
 
 _LAYERS = {}
+_HOSTS = {}
+
+
+def host_layer(layer=0, **kw):
+    """HostLayer cached across tests (its experts are regenerated on first use only); kw: scalar options"""
+    key = (layer, tuple(sorted(kw.items())))
+    if key not in _HOSTS:
+        _HOSTS[key] = HostLayer(layer, **kw)
+    return _HOSTS[key]
 
 
 def gpu_layer(name, dev, **kw):
@@ -109,11 +118,11 @@ def decode_fp32(lay, x, dev, with_shared=True, y0=None):
     return y
 
 
-@pytest.mark.parametrize("R", [1, 4, 8, 16])
+@pytest.mark.parametrize("R", [1, 3, 4, 8, 13, 16])
 def test_decode_layer_parity(dev, R):
     log(f"decode R={R}")
     lay = gpu_layer("c0", dev, layer=0)
-    hl = HostLayer(0)
+    hl = host_layer(0)
     x = synth.gen_x(R, R, dev)
     xn = u16(x)
     assert np.array_equal(xn, x_rows(R, R))
@@ -177,7 +186,7 @@ def test_decode_layer_fused(dev, R):
     """router + experts in the four launches of hmoe_moe_decode_layer; bf16 out = rounded fp32 sum"""
     log(f"fused decode R={R}")
     lay = gpu_layer("c0", dev, layer=0)
-    hl = HostLayer(0)
+    hl = host_layer(0)
     x = synth.gen_x(50 + R, R, dev)
     xn = u16(x)
     y = torch.zeros((R, H), dtype=torch.float32, device=dev)
@@ -188,6 +197,37 @@ def test_decode_layer_fused(dev, R):
     assert np.array_equal(u16(lay.rw[:R]), rw_ref)
     yh = y.cpu().numpy()
     ma, mr = parity(yh, hl.moe(xn, sel_ref, rw_ref))
+    log(f"  max|d| {ma:.3e} mean-rel {mr:.3e}")
+    assert ma <= MAX_ABS and mr <= MEAN_REL
+    assert np.array_equal(u16(out), O.f32_to_bf16(yh))
+
+
+@pytest.mark.parametrize("lo,n_hot", [(64, 160), (256, 256)])
+def test_decode_window_offset(dev, lo, n_hot):
+    """the fused layer with its resident window at an offset, [lo, lo + n_hot) with local id = id - lo, and the
+    shared expert: picks outside the window are skipped; (256, 256) leaves no routed pick at all (the shared expert
+    alone: the kernels' stand-in loads for an empty step)"""
+    R = 5
+    log(f"decode window [{lo}, {lo + n_hot}) R={R}")
+    lay = gpu_layer("c0", dev, layer=0)
+    hl = host_layer(0)
+    x = synth.gen_x(900 + lo, R, dev)
+    xn = u16(x)
+    y = torch.zeros((R, H), dtype=torch.float32, device=dev)
+    saved = lay.lo, lay.n_hot
+    lay.lo, lay.n_hot = lo, n_hot
+    try:
+        out = lay.decode(x, y=y)
+        torch.cuda.synchronize()
+    finally:
+        lay.lo, lay.n_hot = saved
+    sel_ref, rw_ref = hl.route(xn)
+    assert np.array_equal(lay.sel[:R].cpu().numpy(), sel_ref)
+    inside = ((sel_ref >= lo) & (sel_ref < lo + n_hot)).sum()
+    log(f"  picks inside the window: {inside} of {sel_ref.size}")
+    ref = O.moe(0, xn, sel_ref, rw_ref, hl.table(sel_ref, lo), lo, n_hot, hl.shared, threads=16)
+    yh = y.cpu().numpy()
+    ma, mr = parity(yh, ref)
     log(f"  max|d| {ma:.3e} mean-rel {mr:.3e}")
     assert ma <= MAX_ABS and mr <= MEAN_REL
     assert np.array_equal(u16(out), O.f32_to_bf16(yh))
@@ -211,7 +251,7 @@ def test_stack_layers_and_graph(dev):
     h_prev = x.float().cpu().numpy()
     y_prev = None
     for l, (r_after, xn, y, sel, rw) in enumerate(tr):
-        hl = HostLayer(l)
+        hl = host_layer(l)
         r_ref, xn_ref = O.residual_rmsnorm(h_prev, y_prev, ws[l].cpu().numpy(), 1e-5)
         assert np.array_equal(r_after.cpu().numpy().view(np.uint32), r_ref.view(np.uint32))
         assert np.array_equal(u16(xn), xn_ref)
@@ -267,7 +307,7 @@ def test_prefill_parity(dev):
     T = 2048
     log("prefill T=2048")
     lay = gpu_layer("c2", dev, layer=0, bias_sigma=0.001, max_rows=T)
-    hl = HostLayer(0, bias_sigma=0.001)
+    hl = host_layer(0, bias_sigma=0.001)
     x = synth.gen_x(2, T, dev)
     xn = u16(x)
     lay.prefill(x)
@@ -289,4 +329,35 @@ def test_prefill_parity(dev):
     ref = hl.moe(xn[rows], sel_ref[rows], rw_ref[rows])
     ma, mr = parity(yh[rows], ref)
     log(f"  sampled rows max|d| {ma:.3e} mean-rel {mr:.3e}")
+    assert ma <= MAX_ABS and mr <= MEAN_REL
+
+
+@pytest.mark.parametrize("T", [1, 37, 300])
+def test_prefill_ragged(dev, T):
+    """prefill chunks that are not a multiple of the 128-row block (the shared expert's last block partial, experts
+    with one or two picks): routing bit-exact, the router's f16 copy of x exact, the fp32 output of the f16 input path
+    within tolerance on sampled rows (the first and last among them), and the bf16 output its rounding"""
+    log(f"prefill T={T}")
+    lay = gpu_layer("c2", dev, layer=0, bias_sigma=0.001, max_rows=2048)
+    hl = host_layer(0, bias_sigma=0.001)
+    x = synth.gen_x(700 + T, T, dev)
+    xn = u16(x)
+    out = lay.prefill(x).clone()
+    torch.cuda.synchronize()
+    pf = lay._pf
+    sel_ref, rw_ref = hl.route(xn)
+    assert np.array_equal(pf.sel[:T].cpu().numpy(), sel_ref) and np.array_equal(u16(pf.rw[:T]), rw_ref)
+    assert np.array_equal(u16(pf.xh[:T]), O.f32_to_f16(O.bf16_to_f32(xn)))
+    assert int(pf.meta[0].item()) == T * 8
+    y = pf.y[:T]
+    y.zero_()
+    lay.prefill_experts(pf.xh[:T], y)
+    yh = y.cpu().numpy()
+    y.zero_()
+    torch.cuda.synchronize()
+    assert np.array_equal(u16(out), O.f32_to_bf16(yh))
+    extra = np.random.default_rng(T).choice(T, max(min(T, 12) - 2, 0), replace=False)
+    rows = np.unique(np.concatenate([[0, T - 1], extra]))
+    ma, mr = parity(yh[rows], hl.moe(xn[rows], sel_ref[rows], rw_ref[rows]))
+    log(f"  rows {rows.tolist()}: max|d| {ma:.3e} mean-rel {mr:.3e}")
     assert ma <= MAX_ABS and mr <= MEAN_REL
