@@ -20,13 +20,14 @@
 //   gate/up  256 workgroups; each first sums one matrix (gate or up) of one 16-row block of the shared expert over
 //            the full K (its loads go out before the routing prologue and cover it; fp32 sums into act), then
 //            derives the step's routing (top-k from the logits, or the given sel / rw) and the distinct experts
-//            (moe4.cu:86-110) and takes routed items (slot, 16-row block nb) b, b + G, ...; 12 waves each own 4 k
+//            (moe4.cu:86-110), which workgroup 0 records in act for the down launch (slot count, local expert of
+//            each slot), and takes routed items (slot, 16-row block nb) b, b + G, ...; 12 waves each own 4 k
 //            groups of H with the rows' x in registers; the 12 wave partials are summed in wave order through LDS
 //            and act[slot][r][n] = f16(silu(g) u w) is written (moe4.cu:645-676)
-//   down     first the shared expert's 16-row blocks of H (part 0, its act formed from the fp32 sums; no routing
-//            needed, so their loads cover the routing prologue), then routed items (slot quad, 16-row block of H),
-//            contiguous per workgroup; 16 waves = 4 slots x 4 k quarters of I with the slots' act in registers; the
-//            16 partials are summed in order into y32[part] (moe4.cu:443-643)
+//   down     first the shared expert's 16-row blocks of H (part 0, its act formed from the fp32 sums; their loads
+//            cover the read of the routing record), then routed items (slot quad, 16-row block of H), contiguous per
+//            workgroup; 16 waves = 4 slots x 4 k quarters of I with the slots' act in registers; the 16 partials
+//            are summed in order into y32[part] (moe4.cu:443-643)
 //   reduce   y[r] (+)= sum of the parts in order (moe4.cu:826-827 accumulates into y), or the layer's bf16 output
 #include "hmoe_dev.h"
 
@@ -52,15 +53,8 @@ struct Route
     float w[MAXSLOT][MAXR];
 };
 
-// the raw pick of thread t < R * TOPK (sel, rw), read from GLOBAL memory (global address space loads: sel / rw must
-// not be in LDS). The loads are unconditional (index clamped), so a caller can issue them ahead of its weight loads
-// and consume them later.
+// one pick (expert id, f16 routing weight) of the step
 struct Pick { int64_t s; uint16_t w; };
-__device__ __forceinline__ Pick load_pick_global(const int64_t* sel, const uint16_t* rw, int R)
-{
-    const int i = min((int) threadIdx.x, R * TOPK - 1);
-    return {ldg<int64_t>(sel + i), ldg<uint16_t>(rw + i)};
-}
 
 // distinct experts of the step (ascending local id) and routing weight per (slot, row): moe4.cu:86-110, with the slot
 // of each pick from popcounts of the 256-bit mask. Ends with a barrier.
@@ -126,13 +120,11 @@ __device__ __forceinline__ void group_i4(const f16x8* xa, u32x4 wq, float s, f32
     for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(s, p[i], acc[i]);
 }
 
-// ---- router logits: two experts per 512-thread workgroup (expert_logits) ----
+// ---- router logits: two experts per 512-thread workgroup (pair_logits_h) ----
 __global__ void __launch_bounds__(NT) router_kernel(const uint16_t* __restrict__ x, int R, const float* __restrict__ wt,
                                                     int E, float* __restrict__ logits)
 {
-    __shared__ float sums[2][256][MAXR + 1];
-    const int half = threadIdx.x >> 8, tid = threadIdx.x & 255;
-    expert_logits(x, wt, 2 * blockIdx.x + half, E, R, H, tid, sums[half], logits);
+    pair_logits_h(x, wt, 2 * blockIdx.x, E, R, logits);
 }
 
 // ---- gate/up: the shared expert's unit first (it needs no routing), then the routed items ----
@@ -230,6 +222,13 @@ __global__ void __launch_bounds__(GW * 64) gu7_kernel(
         const int e = rt.e[threadIdx.x];
         ptr[0][threadIdx.x] = tab[0][e]; ptr[1][threadIdx.x] = tab[1][e];
         ptr[2][threadIdx.x] = tab[2][e]; ptr[3][threadIdx.x] = tab[3][e];
+    }
+    // the routing record for the down launch: m and the local expert id of every slot
+    if (b == 0)
+    {
+        int* rec = (int*) (act + (size_t) REC_SLOT * MAXR * I);
+        if (threadIdx.x == 0) rec[0] = m;
+        if (threadIdx.x < m) rec[REC_E + threadIdx.x] = rt.e[threadIdx.x];
     }
     // no routed expert: slot 0 stands in as the shared matrix (25 MB, beyond every offset a stand-in load reaches)
     if (m == 0 && threadIdx.x < 4) ptr[threadIdx.x][0] = shm;
@@ -340,11 +339,10 @@ constexpr int DN_GMIN = NB_H / 2, DN_GMAX = NB_H;   // grid range: one or two sh
 // gate and up sums the gate/up launch left in the SHP_SLOT area of act.
 template <bool SH>
 __global__ void __launch_bounds__(DW * 64) dn6_kernel(
-    const int64_t* __restrict__ sel, const uint16_t* __restrict__ rw, int R, int lo, int n_hot,
-    const int64_t* __restrict__ down_w, const int64_t* __restrict__ down_s, const _Float16* __restrict__ act,
-    const uint8_t* __restrict__ sh_dw, float* __restrict__ y32, int* __restrict__ nparts_out)
+    int R, int n_hot, const int64_t* __restrict__ down_w, const int64_t* __restrict__ down_s,
+    const _Float16* __restrict__ act, const uint8_t* __restrict__ sh_dw, float* __restrict__ y32,
+    int* __restrict__ nparts_out)
 {
-    __shared__ Route rt;
     __shared__ const uint8_t* tab[2][HMOE_MAXE];
     __shared__ const uint8_t* ptr[2][MAXSLOT];
     __shared__ f32x4 red[2][DW][64];
@@ -354,12 +352,15 @@ __global__ void __launch_bounds__(DW * 64) dn6_kernel(
     const int G = gridDim.x, b = blockIdx.x;
     const int part0 = SH ? 1 : 0, nsh = SH ? NB_H : 0;
     const int s_mine = SH ? (b + G < NB_H ? 2 : 1) : 0;       // (G <= NB_H: every workgroup has one)
-    // loads in issue order: pointer tables, picks, the shared act, the shared items (all independent of routing)
+    // loads in issue order: pointer tables, the gate/up launch's routing record (slot count and the local expert of
+    // each slot), the shared act, the shared items (all independent of routing)
     // (every load here is unconditional, with a valid stand-in address where there is nothing to load: a load under a
     // branch makes the compiler wait for all outstanding loads where the paths meet)
     const int te = min((int) threadIdx.x, max(n_hot - 1, 0));
-    const int64_t t0 = ldg<int64_t>(n_hot > 0 ? down_w + te : sel), t1 = ldg<int64_t>(n_hot > 0 ? down_s + te : sel);
-    const Pick pk = load_pick_global(sel, rw, R);
+    const int* rec = (const int*) (act + (size_t) REC_SLOT * MAXR * I);
+    const int64_t t0 = ldg<int64_t>(n_hot > 0 ? down_w + te : (const int64_t*) rec);
+    const int64_t t1 = ldg<int64_t>(n_hot > 0 ? down_s + te : (const int64_t*) rec);
+    const int rm = ldg<int>(rec), re = ldg<int>(rec + REC_E + min((int) threadIdx.x, MAXSLOT - 1));
     __builtin_amdgcn_sched_barrier(0);                          // keep the routing loads ahead of the item loads
     // shared items: wave w owns k group w of I (4 k steps of F16T) with the shared act of its k group as the A operand,
     // formed from the fp32 sums (loaded first, so forming it does not wait for the tiles); the second item is the
@@ -395,15 +396,19 @@ __global__ void __launch_bounds__(DW * 64) dn6_kernel(
             }
             xs[t] = live ? v : (f16x8) {};
         }
+        // formed here, before the barriers below: sunk to its use, the fp32 sums would stay live next to the shared
+        // tiles and push those into scratch
+        #pragma unroll
+        for (int t = 0; t < 4; ++t) asm volatile("" :: "v"(__builtin_bit_cast(u32x4, xs[t])));
     }
     // every thread stores (threads past n_hot repeat entry n_hot - 1 with its own value): a store under a branch
     // would pull the table loads into it, behind the item loads
     tab[0][te] = (const uint8_t*) t0; tab[1][te] = (const uint8_t*) t1;
-    route_picks(pk, R, lo, n_hot, rt);
-    const int m = rt.m, nq = (m + 3) / 4;
+    __syncthreads();
+    const int m = min(max(rm, 0), min(n_hot, MAXSLOT)), nq = (m + 3) / 4;
     if (threadIdx.x < m)
     {
-        const int e = rt.e[threadIdx.x];
+        const int e = min(max(re, 0), n_hot - 1);
         ptr[0][threadIdx.x] = tab[0][e]; ptr[1][threadIdx.x] = tab[1][e];
     }
     // no routed expert: slot 0 stands in as act, so the first routed load below stays unconditional and in bounds
@@ -569,8 +574,6 @@ static int run_decode(const DecodeArgs& a, int phases, hipStream_t st)
     const int G = a.blocks ? a.blocks : default_grid(1);
     if ((phases & 1) && a.logits)
         router_kernel<<<(a.E + 1) / 2, NT, 0, st>>>((const uint16_t*) a.x, R, a.wt, a.E, a.logits);
-    const int64_t* sel = a.logits ? a.sel_out : a.sel_in;
-    const uint16_t* rw = a.logits ? a.rw_out : a.rw_in;
     if (phases & 2)
     {
         int64_t* so = a.logits ? a.sel_out : (int64_t*) a.sel_in;
@@ -588,11 +591,10 @@ static int run_decode(const DecodeArgs& a, int phases, hipStream_t st)
     {
         const int gd = min(max(G, DN_GMIN), DN_GMAX);
         if (sh)
-            dn6_kernel<true><<<gd, DW * 64, 0, st>>>(sel, rw, R, a.lo, a.n_hot, a.down_w, a.down_s, a.act,
-                                                     (const uint8_t*) a.sh_dw, a.y32, a.ctr);
+            dn6_kernel<true><<<gd, DW * 64, 0, st>>>(R, a.n_hot, a.down_w, a.down_s, a.act, (const uint8_t*) a.sh_dw,
+                                                     a.y32, a.ctr);
         else
-            dn6_kernel<false><<<gd, DW * 64, 0, st>>>(sel, rw, R, a.lo, a.n_hot, a.down_w, a.down_s, a.act, nullptr,
-                                                      a.y32, a.ctr);
+            dn6_kernel<false><<<gd, DW * 64, 0, st>>>(R, a.n_hot, a.down_w, a.down_s, a.act, nullptr, a.y32, a.ctr);
     }
     if (phases & 8) dec_d_kernel<<<(R * H / 4 + 255) / 256, 256, 0, st>>>(a.y32, a.ctr, R, a.y, a.out);
     return HMOE_LAUNCHED("moe4");
@@ -682,7 +684,8 @@ extern "C" int hmoe_moe_decode_layer(const void* x, const float* wt, const float
                                      void* stream)
 {
     (void) gu32;
-    HMOE_REQUIRE(wt && logits && sel && rw && E >= TOPK && E <= RMAXE && topk == TOPK, "decode_layer: router arguments");
+    HMOE_REQUIRE(wt && logits && sel && rw && E >= TOPK && E <= RMAXE && topk == TOPK && ((uintptr_t) wt & 15) == 0,
+                 "decode_layer: router arguments");
     HMOE_REQUIRE(y || out, "decode_layer: no output");
     HMOE_REQUIRE(phases >= 1 && phases <= 15, "decode_layer: phases %d", phases);
     DecodeArgs a = forward_args(x, nullptr, nullptr, R, n_hot, gate_w, up_w, down_w, gate_s, up_s, down_s, act, ctr_a,

@@ -18,7 +18,9 @@ namespace hmoe {
 constexpr int H = HMOE_H, I = HMOE_I, TOPK = HMOE_TOPK, MAXR = HMOE_MAXR, MAXSLOT = HMOE_MAXSLOT;
 constexpr int SH_SLOT = MAXSLOT;            // act slot of the shared expert
 constexpr int SHP_SLOT = MAXSLOT + 1;       // the shared expert's fp32 gate and up sums [2][MAXR][I] (4 slots' room)
-constexpr int ACT_SLOTS = MAXSLOT + 1 + 4;
+constexpr int REC_SLOT = SHP_SLOT + 4;      // the gate/up launch's routing record for the down launch (int words)
+constexpr int ACT_SLOTS = REC_SLOT + 1;
+constexpr int REC_E = 64;                   // record: word 0 = distinct experts m, words REC_E + j = local id of slot j
 
 // ---- error state of the C ABI (common.hip) ----
 int set_error(int code, const char* fmt, ...);
@@ -249,6 +251,111 @@ __device__ inline void expert_logits(const uint16_t* __restrict__ x, const float
             t = t + seg;
         }
         logits[(size_t) tid * RMAXE + e] = t;
+    }
+}
+
+// logits of experts e0 and e0 + 1 (those < E) for R <= MAXR rows over K = H, by a 512-thread workgroup, in the order of
+// expert_logits with every global load coalesced: the two weight rows, then each group of 4 rows of x, are staged in
+// LDS (consecutive threads on consecutive 16-byte pieces) in a chunk-major layout padded to 144 B (weights) and 80 B
+// (x) per chunk, so a thread's 16-byte reads of its own chunk are free of bank conflicts (8 lanes cover the 32 banks);
+// thread c < 192 of half h runs the fmaf chain of chunk c for expert e0 + h. (Read straight from global memory, a lane
+// takes its chunk's 64 or 128 contiguous bytes in 16-byte steps, and each load instruction touches 64 cache lines.)
+// Every thread of the workgroup must call it (it contains barriers).
+constexpr int LCH = H / RCHUNK;             // 192 chunks
+constexpr int WST = RCHUNK + 4;             // weight chunk stride, floats
+constexpr int XST = RCHUNK / 2 + 4;         // x chunk stride, u32 words (two bf16 each)
+__device__ inline void pair_logits_h(const uint16_t* __restrict__ x, const float* __restrict__ wt, int e0, int E, int R,
+                                     float* __restrict__ logits)
+{
+    __shared__ __attribute__((aligned(16))) float ws[2][LCH * WST];
+    __shared__ __attribute__((aligned(16))) uint32_t xs[4][LCH * XST];
+    __shared__ float sums[2][LCH][MAXR + 1];
+    __shared__ float segs[2][MAXR][RSEG];
+    const int t = threadIdx.x, half = t >> 8, c = t & 255;
+    // the two weight rows: 2 x 1536 pieces of 4 floats, 6 per thread (a row past E re-reads row E - 1)
+    #pragma unroll
+    for (int i = 0; i < 6; ++i)
+    {
+        const int p = t + 512 * i, h = p / 1536, q = p - h * 1536;
+        const f32x4 v = *(const f32x4*) (wt + (size_t) min(e0 + h, E - 1) * H + 4 * q);
+        *(f32x4*) &ws[h][(q >> 3) * WST + 4 * (q & 7)] = v;
+    }
+    // rows r0 .. r0 + 3 of x: 4 x 768 pieces of 8 bf16, 6 per thread (rows past R re-read row R - 1); the next
+    // group's loads are in flight while the current group computes
+    u32x4 nx[6];
+    auto load_x = [&](int r0) {
+        #pragma unroll
+        for (int i = 0; i < 6; ++i)
+        {
+            const int p = t + 512 * i, j = p / 768, q = p - j * 768;
+            nx[i] = *(const u32x4*) (x + (size_t) min(r0 + j, R - 1) * H + 8 * q);
+        }
+    };
+    auto store_x = [&]() {
+        #pragma unroll
+        for (int i = 0; i < 6; ++i)
+        {
+            const int p = t + 512 * i, j = p / 768, q = p - j * 768;
+            *(u32x4*) &xs[j][(q >> 2) * XST + 4 * (q & 3)] = nx[i];
+        }
+    };
+    load_x(0);
+    store_x();
+    float wv[RCHUNK];
+    for (int r0 = 0; r0 < R; r0 += 4)
+    {
+        __syncthreads();                                        // group r0 in xs
+        load_x(r0 + 4);
+        if (c < LCH)
+        {
+            if (r0 == 0)
+            {
+                #pragma unroll
+                for (int i = 0; i < RCHUNK; i += 4)
+                {
+                    const f32x4 v = *(const f32x4*) &ws[half][c * WST + i];
+                    wv[i] = v[0]; wv[i + 1] = v[1]; wv[i + 2] = v[2]; wv[i + 3] = v[3];
+                }
+            }
+            #pragma unroll
+            for (int j = 0; j < 4; ++j)
+            {
+                if (r0 + j >= R) break;
+                u32x4 xv[4];
+                #pragma unroll
+                for (int i = 0; i < 4; ++i) xv[i] = *(const u32x4*) &xs[j][c * XST + 4 * i];
+                float acc = 0.f;
+                #pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    #pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                    {
+                        acc = __builtin_fmaf(__uint_as_float(xv[i][k] << 16), wv[8 * i + 2 * k], acc);
+                        acc = __builtin_fmaf(__uint_as_float(xv[i][k] & 0xffff0000u), wv[8 * i + 2 * k + 1], acc);
+                    }
+                sums[half][c][r0 + j] = acc;
+            }
+        }
+        __syncthreads();                                        // every read of xs done
+        store_x();
+    }
+    // the fold: segment sums (chunks in order) by one thread per (expert, row, segment), then the segments in order
+    constexpr int cps = LCH / RSEG;
+    if (t < 2 * R * RSEG)
+    {
+        const int h = t / (R * RSEG), rem = t - h * R * RSEG, r = rem / RSEG, sg = rem - r * RSEG;
+        float seg = 0.f;
+        #pragma unroll
+        for (int q = 0; q < cps; ++q) seg = seg + sums[h][sg * cps + q][r];
+        segs[h][r][sg] = seg;
+    }
+    __syncthreads();
+    if (e0 + half < E && c < R)
+    {
+        float tot = 0.f;
+        #pragma unroll
+        for (int sg = 0; sg < RSEG; ++sg) tot = tot + segs[half][c][sg];
+        logits[(size_t) c * RMAXE + e0 + half] = tot;
     }
 }
 

@@ -12,7 +12,20 @@
 namespace hmoe {
 
 
-// small path, 1: two experts per 512-thread workgroup (expert_logits), optional f16 copy of x
+// small path, 1: two experts per 512-thread workgroup, optional f16 copy of x; K = H through LDS (pair_logits_h),
+// other K straight from global memory (expert_logits)
+__global__ void __launch_bounds__(512) router_logits_h_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ wt, float* __restrict__ logits, int R, int E,
+    _Float16* __restrict__ xh)
+{
+    pair_logits_h(x, wt, 2 * blockIdx.x, E, R, logits);
+    if (xh)
+    {
+        const int n = R * H, per = (n + gridDim.x - 1) / gridDim.x, b0 = blockIdx.x * per;
+        to_f16_range(x, xh, b0, min(n, b0 + per), threadIdx.x, blockDim.x);
+    }
+}
+
 __global__ void __launch_bounds__(512) router_logits_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ wt, float* __restrict__ logits, int R, int K, int E,
     _Float16* __restrict__ xh)
@@ -158,7 +171,10 @@ extern "C" int hmoe_router_fused(const void* x, const float* wt, const float* bi
     hipStream_t st = (hipStream_t) stream;
     if (R <= MAXR)
     {
-        router_logits_kernel<<<(E + 1) / 2, 512, 0, st>>>((const uint16_t*) x, wt, logits, R, K, E, (_Float16*) xh);
+        if (K == H)
+            router_logits_h_kernel<<<(E + 1) / 2, 512, 0, st>>>((const uint16_t*) x, wt, logits, R, E, (_Float16*) xh);
+        else
+            router_logits_kernel<<<(E + 1) / 2, 512, 0, st>>>((const uint16_t*) x, wt, logits, R, K, E, (_Float16*) xh);
         router_select_small_kernel<<<1, 1024, 0, st>>>(logits, bias, R, E, topk, scale, sel, rw);
         return HMOE_LAUNCHED("router_fused");
     }

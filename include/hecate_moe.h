@@ -92,8 +92,10 @@ int hmoe_moe4_forward(const void* x, const int64_t* sel, const uint16_t* rw, int
                       int lo, const void* sh_gw, const void* sh_uw, const void* sh_dw, const void* sh_gs,
                       const void* sh_us, const void* sh_ds, int xf, void* stream);
 /* the two phases of hmoe_moe4_forward, for callers that time or schedule them apart (this build's addition):
- * gate_up writes act (with the shared expert: also its fp32 gate and up sums, in act), down adds into y (ctr_b
- * carries its part count); same arguments and rules as forward */
+ * gate_up writes act (with the shared expert: also its fp32 gate and up sums, in act) and, in act, the step's routing
+ * record (distinct expert count and the local expert of each act slot); down adds into y (ctr_b carries its part
+ * count), taking the slots from that record, so it must follow a gate_up of the same step on the same act (sel, rw
+ * and lo are accepted for the argument positions); same arguments and rules as forward otherwise */
 int hmoe_moe4_gate_up(const void* x, const int64_t* sel, const uint16_t* rw, int R, int n_hot,
                       const int64_t* gate_w, const int64_t* up_w, const int64_t* gate_s, const int64_t* up_s,
                       void* act, float* gu32, int* ctr_a, int blocks, int lo, const void* sh_gw, const void* sh_uw,
