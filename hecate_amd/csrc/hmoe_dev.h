@@ -131,8 +131,27 @@ __device__ __forceinline__ void load_bias_global(const float* __restrict__ bias,
     }
 }
 
-// top-k of one row by a wave: keys of experts lane + 64 i; each round takes the largest (key, -index) pair, so ties
-// go to the lowest index (exl3_router.py:106-121); the sum runs over the selected unbiased activations in order
+// (hi, lo) <- the larger of the 64-bit keys (hi, lo) and (h2, l2)
+__device__ __forceinline__ void max_key(uint32_t& hi, uint32_t& lo, uint32_t h2, uint32_t l2)
+{
+    const bool gt = h2 > hi || (h2 == hi && l2 > lo);
+    hi = gt ? h2 : hi;
+    lo = gt ? l2 : lo;
+}
+// one step of a 16-lane row reduction: combine with the key of the lane DPP control CTRL names (the quad permutations
+// and row rotations used here keep every source lane inside the row)
+template <int CTRL>
+__device__ __forceinline__ void max_key_dpp(uint32_t& hi, uint32_t& lo)
+{
+    const uint32_t h2 = (uint32_t) __builtin_amdgcn_mov_dpp((int) hi, CTRL, 0xf, 0xf, false);
+    const uint32_t l2 = (uint32_t) __builtin_amdgcn_mov_dpp((int) lo, CTRL, 0xf, 0xf, false);
+    max_key(hi, lo, h2, l2);
+}
+
+// top-k of one row by a wave (all 64 lanes active): keys of experts lane + 64 i; each round takes the largest
+// (key, -index) pair, so ties go to the lowest index (exl3_router.py:106-121); the sum runs over the selected unbiased
+// activations in order. A round reduces each 16-lane row with DPP (lane pairs, quad pairs, rotations by 4 and 8) and
+// the four row maxima in scalar registers, so the winner is wave-uniform.
 __device__ inline void select_from(const RowIn& in, int E, int topk, float scale, int64_t* __restrict__ sel,
                                    uint16_t* __restrict__ rw)
 {
@@ -152,28 +171,22 @@ __device__ inline void select_from(const RowIn& in, int E, int topk, float scale
     float sum = 0.f, wsel = 0.f; int isel = 0;
     for (int k = 0; k < topk; ++k)
     {
-        uint64_t best = 0ull;
+        uint32_t hi = key[0], lo = 0xffffu - lane;
         #pragma unroll
-        for (int i = 0; i < 4; ++i)
-        {
-            const uint64_t v = ((uint64_t) key[i] << 32) | (uint32_t) (0xffffu - (lane + 64 * i));
-            best = v > best ? v : best;
-        }
+        for (int i = 1; i < 4; ++i) max_key(hi, lo, key[i], 0xffffu - (lane + 64 * i));
+        max_key_dpp<0xb1>(hi, lo);                               // quad_perm [1, 0, 3, 2]
+        max_key_dpp<0x4e>(hi, lo);                               // quad_perm [2, 3, 0, 1]
+        max_key_dpp<0x124>(hi, lo);                              // row_ror 4
+        max_key_dpp<0x128>(hi, lo);                              // row_ror 8
+        uint32_t bh = __builtin_amdgcn_readlane(hi, 0), bl = __builtin_amdgcn_readlane(lo, 0);
         #pragma unroll
-        for (int off = 32; off > 0; off >>= 1)
-        {
-            const uint32_t lo = __shfl_xor((uint32_t) best, off), hi = __shfl_xor((uint32_t) (best >> 32), off);
-            const uint64_t o = ((uint64_t) hi << 32) | lo;
-            best = o > best ? o : best;
-        }
-        const int e = 0xffff - (int) (best & 0xffffu);
-        float mine = 0.f;
-        if ((e & 63) == lane)
-        {
-            #pragma unroll
-            for (int i = 0; i < 4; ++i) if (i == (e >> 6)) { mine = a[i]; key[i] = 0u; }
-        }
-        const float av = __shfl(mine, e & 63);
+        for (int r = 1; r < 4; ++r)
+            max_key(bh, bl, __builtin_amdgcn_readlane(hi, 16 * r), __builtin_amdgcn_readlane(lo, 16 * r));
+        const int e = 0xffff - (int) (bl & 0xffffu), wl = e & 63, wi = e >> 6;
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) key[i] = (lane == wl && i == wi) ? 0u : key[i];
+        const float aw = wi == 0 ? a[0] : (wi == 1 ? a[1] : (wi == 2 ? a[2] : a[3]));
+        const float av = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(aw), wl));
         sum = sum + av;
         if (lane == k) { wsel = av; isel = e; }
     }
