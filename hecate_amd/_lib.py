@@ -39,6 +39,7 @@ SIGNATURES = {
     "hmoe_moe4p_forward": (i32, [P, P, P, P, P, i32, i32, i32, P, P, P, P, P, P, P, P, P, P, i32, P, P, i32, i32,
                                  P, P, P, i32, P]),
     "hmoe_residual_rmsnorm": (i32, [P, P, P, i32, f32, P, P, P]),
+    "hmoe_norm_router": (i32, [P, P, f32, i32, P, i32, P, P, P, P]),
 }
 
 

@@ -120,11 +120,18 @@ __device__ __forceinline__ void group_i4(const f16x8* xa, u32x4 wq, float s, f32
     for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(s, p[i], acc[i]);
 }
 
-// ---- router logits: two experts per 512-thread workgroup (pair_logits_h) ----
+// ---- router logits: two experts per 512-thread workgroup (pair_logits) ----
 __global__ void __launch_bounds__(NT) router_kernel(const uint16_t* __restrict__ x, int R, const float* __restrict__ wt,
                                                     int E, float* __restrict__ logits)
 {
-    pair_logits_h(x, wt, 2 * blockIdx.x, E, R, logits);
+    pair_logits<false>(x, NormIn{}, wt, 2 * blockIdx.x, E, R, logits);
+}
+
+// ---- RMSNorm of the residual + router logits (nr4_kernel.cuh:122-381), the same workgroups ----
+__global__ void __launch_bounds__(NT) norm_router_kernel(NormIn nin, int R, const float* __restrict__ wt, int E,
+                                                         float* __restrict__ logits)
+{
+    pair_logits<true>(nullptr, nin, wt, 2 * blockIdx.x, E, R, logits);
 }
 
 // ---- gate/up: the shared expert's unit first (it needs no routing), then the routed items ----
@@ -673,6 +680,18 @@ extern "C" int hmoe_moe4_forward(const void* x, const int64_t* sel, const uint16
     if (rc) return rc;
     HMOE_REQUIRE(sel && rw && y, "moe4_forward: null buffer");
     return run_decode(a, 15, (hipStream_t) stream);
+}
+
+extern "C" int hmoe_norm_router(const float* h, const float* norm_w, float eps, int R, const float* wt, int E,
+                                float* logits, uint16_t* xn, void* xh, void* stream)
+{
+    HMOE_REQUIRE(h && norm_w && wt && logits && xn && R >= 1 && R <= MAXR && E >= TOPK && E <= RMAXE,
+                 "norm_router: arguments (rows %d experts %d)", R, E);
+    HMOE_REQUIRE(((uintptr_t) h & 15) == 0 && ((uintptr_t) norm_w & 15) == 0 && ((uintptr_t) wt & 15) == 0 &&
+                 ((uintptr_t) xn & 15) == 0 && ((uintptr_t) xh & 15) == 0, "norm_router: alignment");
+    norm_router_kernel<<<(E + 1) / 2, NT, 0, (hipStream_t) stream>>>(NormIn{h, norm_w, eps, xn, (_Float16*) xh}, R, wt,
+                                                                     E, logits);
+    return HMOE_LAUNCHED("norm_router");
 }
 
 extern "C" int hmoe_moe_decode_layer(const void* x, const float* wt, const float* bias, int E, int topk, float scale,

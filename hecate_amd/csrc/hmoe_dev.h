@@ -267,23 +267,39 @@ __device__ inline void expert_logits(const uint16_t* __restrict__ x, const float
     }
 }
 
+// The fused input path of the router (nr4_kernel.cuh:122-381: RMSNorm + router in one launch): the residual h fp32
+// [R][H] and the norm weight w; xn = bf16((h * rmf) * w) with rmf = 1 / sqrt(sum_k h^2 / H + eps), the sum in the
+// order of the residual + RMSNorm kernel (256 fmaf chains over k = c, c + 256, ..., folded by halving), so xn is
+// bit-identical to that kernel's. Each workgroup writes its slice of xn (and of xh, the f16 copy, when not NULL).
+struct NormIn
+{
+    const float* h;
+    const float* w;
+    float eps;
+    uint16_t* xn;
+    _Float16* xh;
+};
+
 // logits of experts e0 and e0 + 1 (those < E) for R <= MAXR rows over K = H, by a 512-thread workgroup, in the order of
 // expert_logits with every global load coalesced: the two weight rows, then each group of 4 rows of x, are staged in
 // LDS (consecutive threads on consecutive 16-byte pieces) in a chunk-major layout padded to 144 B (weights) and 80 B
 // (x) per chunk, so a thread's 16-byte reads of its own chunk are free of bank conflicts (8 lanes cover the 32 banks);
 // thread c < 192 of half h runs the fmaf chain of chunk c for expert e0 + h. (Read straight from global memory, a lane
 // takes its chunk's 64 or 128 contiguous bytes in 16-byte steps, and each load instruction touches 64 cache lines.)
-// Every thread of the workgroup must call it (it contains barriers).
+// NORM: x is formed from the residual (NormIn) instead of read as bf16. Every thread of the workgroup must call it
+// (it contains barriers).
 constexpr int LCH = H / RCHUNK;             // 192 chunks
 constexpr int WST = RCHUNK + 4;             // weight chunk stride, floats
 constexpr int XST = RCHUNK / 2 + 4;         // x chunk stride, u32 words (two bf16 each)
-__device__ inline void pair_logits_h(const uint16_t* __restrict__ x, const float* __restrict__ wt, int e0, int E, int R,
-                                     float* __restrict__ logits)
+template <bool NORM>
+__device__ inline void pair_logits(const uint16_t* __restrict__ x, const NormIn& nin, const float* __restrict__ wt,
+                                   int e0, int E, int R, float* __restrict__ logits)
 {
     __shared__ __attribute__((aligned(16))) float ws[2][LCH * WST];
     __shared__ __attribute__((aligned(16))) uint32_t xs[4][LCH * XST];
-    __shared__ float sums[2][LCH][MAXR + 1];
+    __shared__ __attribute__((aligned(16))) float sums[2][LCH][MAXR + 1];
     __shared__ float segs[2][MAXR][RSEG];
+    __shared__ float rmfs[MAXR];
     const int t = threadIdx.x, half = t >> 8, c = t & 255;
     // the two weight rows: 2 x 1536 pieces of 4 floats, 6 per thread (a row past E re-reads row E - 1)
     #pragma unroll
@@ -293,8 +309,34 @@ __device__ inline void pair_logits_h(const uint16_t* __restrict__ x, const float
         const f32x4 v = *(const f32x4*) (wt + (size_t) min(e0 + h, E - 1) * H + 4 * q);
         *(f32x4*) &ws[h][(q >> 3) * WST + 4 * (q & 7)] = v;
     }
+    if (NORM)
+    {
+        // rmf of every row: chain c of row r by thread (r % 2) * 256 + c, the halving fold in sums (as [R][256])
+        float (*part)[256] = reinterpret_cast<float (*)[256]>(&sums[0][0][0]);
+        for (int r = half; r < R; r += 2)
+        {
+            const float* v = nin.h + (size_t) r * H + c;
+            float hv[H / 256];
+            #pragma unroll
+            for (int j = 0; j < H / 256; ++j) hv[j] = v[256 * j];
+            float p = 0.f;
+            #pragma unroll
+            for (int j = 0; j < H / 256; ++j) p = __builtin_fmaf(hv[j], hv[j], p);
+            part[r][c] = p;
+        }
+        __syncthreads();
+        for (int off = 128; off > 0; off >>= 1)
+        {
+            for (int r = half; r < R; r += 2)
+                if (c < off) part[r][c] = part[r][c] + part[r][c + off];
+            __syncthreads();
+        }
+        if (t < R) rmfs[t] = 1.0f / __builtin_sqrtf(part[t][0] / (float) H + nin.eps);
+        __syncthreads();                                        // (sums is written again by the chains below)
+    }
     // rows r0 .. r0 + 3 of x: 4 x 768 pieces of 8 bf16, 6 per thread (rows past R re-read row R - 1); the next
-    // group's loads are in flight while the current group computes
+    // group's loads are in flight while the current group computes (NORM: formed at the start of each group, and
+    // piece q of a live row also stored to xn by workgroup q * G / 768)
     u32x4 nx[6];
     auto load_x = [&](int r0) {
         #pragma unroll
@@ -312,13 +354,52 @@ __device__ inline void pair_logits_h(const uint16_t* __restrict__ x, const float
             *(u32x4*) &xs[j][(q >> 2) * XST + 4 * (q & 3)] = nx[i];
         }
     };
-    load_x(0);
-    store_x();
+    auto form_x = [&](int r0) {
+        #pragma unroll
+        for (int i = 0; i < 6; ++i)
+        {
+            const int p = t + 512 * i, j = p / 768, q = p - j * 768, row = min(r0 + j, R - 1);
+            const float* hp = nin.h + (size_t) row * H + 8 * q;
+            const f32x4 h0 = *(const f32x4*) hp, h1 = *(const f32x4*) (hp + 4);
+            const f32x4 w0 = *(const f32x4*) (nin.w + 8 * q), w1 = *(const f32x4*) (nin.w + 8 * q + 4);
+            const float rf = rmfs[row];
+            u32x4 v;
+            #pragma unroll
+            for (int e = 0; e < 4; ++e)
+            {
+                const float a0 = e < 2 ? h0[2 * e] : h1[2 * e - 4], a1 = e < 2 ? h0[2 * e + 1] : h1[2 * e - 3];
+                const float b0 = e < 2 ? w0[2 * e] : w1[2 * e - 4], b1 = e < 2 ? w0[2 * e + 1] : w1[2 * e - 3];
+                v[e] = (uint32_t) hmoe_f2bf((a0 * rf) * b0) | ((uint32_t) hmoe_f2bf((a1 * rf) * b1) << 16);
+            }
+            *(u32x4*) &xs[j][(q >> 2) * XST + 4 * (q & 3)] = v;
+            if (r0 + j < R && (int) ((q * gridDim.x) / 768) == (int) blockIdx.x)
+            {
+                *(u32x4*) (nin.xn + (size_t) row * H + 8 * q) = v;
+                if (nin.xh)
+                {
+                    f16x8 o;
+                    #pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                    {
+                        o[2 * e] = (_Float16) __uint_as_float(v[e] << 16);
+                        o[2 * e + 1] = (_Float16) __uint_as_float(v[e] & 0xffff0000u);
+                    }
+                    *(f16x8*) (nin.xh + (size_t) row * H + 8 * q) = o;
+                }
+            }
+        }
+    };
+    if (!NORM)
+    {
+        load_x(0);
+        store_x();
+    }
     float wv[RCHUNK];
     for (int r0 = 0; r0 < R; r0 += 4)
     {
+        if (NORM) form_x(r0);
         __syncthreads();                                        // group r0 in xs
-        load_x(r0 + 4);
+        if (!NORM) load_x(r0 + 4);
         if (c < LCH)
         {
             if (r0 == 0)
@@ -350,7 +431,7 @@ __device__ inline void pair_logits_h(const uint16_t* __restrict__ x, const float
             }
         }
         __syncthreads();                                        // every read of xs done
-        store_x();
+        if (!NORM) store_x();
     }
     // the fold: segment sums (chunks in order) by one thread per (expert, row, segment), then the segments in order
     constexpr int cps = LCH / RSEG;

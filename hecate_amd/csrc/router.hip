@@ -12,13 +12,13 @@
 namespace hmoe {
 
 
-// small path, 1: two experts per 512-thread workgroup, optional f16 copy of x; K = H through LDS (pair_logits_h),
+// small path, 1: two experts per 512-thread workgroup, optional f16 copy of x; K = H through LDS (pair_logits),
 // other K straight from global memory (expert_logits)
 __global__ void __launch_bounds__(512) router_logits_h_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ wt, float* __restrict__ logits, int R, int E,
     _Float16* __restrict__ xh)
 {
-    pair_logits_h(x, wt, 2 * blockIdx.x, E, R, logits);
+    pair_logits<false>(x, NormIn{}, wt, 2 * blockIdx.x, E, R, logits);
     if (xh)
     {
         const int n = R * H, per = (n + gridDim.x - 1) / gridDim.x, b0 = blockIdx.x * per;

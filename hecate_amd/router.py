@@ -26,3 +26,18 @@ def router_fused(x, wt, bias, logits, ctr, sel, rw, topk, scale, xh=None):
     call("hmoe_router_fused", ptr(x), ptr(wt), ptr(bias), ptr(logits), ptr(ctr), ptr(sel), ptr(rw), int(R), int(K),
          int(E), int(topk), float(scale), ptr(xh), stream_of(x.device))
     return sel, rw
+
+
+def norm_router(h, norm_w, eps, wt, logits, xn, xh=None):
+    """nr4_kernel.cuh:122-381 (RMSNorm + router scores in one launch) for the decode path: xn = bf16 RMSNorm(h) * norm_w
+    (bit-identical to hmoe_residual_rmsnorm without a residual add) and the router logits of xn into logits (the
+    layout MoELayer.decode reads with phases=14); h fp32 [R, H], R <= 16"""
+    R, K = h.shape
+    E = wt.shape[0]
+    if not (h.dtype == torch.float32 and norm_w.dtype == torch.float32 and wt.dtype == torch.float32
+            and xn.dtype == torch.bfloat16 and h.is_contiguous() and xn.is_contiguous() and xn.shape == h.shape
+            and 1 <= R <= 16 and logits.numel() * 4 >= int(lib().hmoe_router_scratch_bytes(R, E))):
+        raise RuntimeError("norm_router: shape / dtype")
+    call("hmoe_norm_router", ptr(h), ptr(norm_w), float(eps), int(R), ptr(wt), int(E), ptr(logits), ptr(xn), ptr(xh),
+         stream_of(h.device))
+    return xn

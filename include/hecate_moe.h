@@ -159,6 +159,14 @@ int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid, const floa
  * rmf = 1 / sqrt(sum / H + eps), xn = bf16((r * rmf) * w); xh optional f16 copy of xn. */
 int hmoe_residual_rmsnorm(float* r, float* a, const float* w, int R, float eps, uint16_t* xn, uint16_t* xh,
                           void* stream);
+/* ---- RMSNorm + router in one launch: runtime/tier/nr4_kernel.cuh:122-381 (nr4_kernel: norm, router scores) ----
+ * h fp32 [R][H] (the residual, read only; R <= 16), norm_w fp32 [H]: xn = bf16(h * rsqrt(mean h^2 + eps) * norm_w) in
+ * the order of hmoe_residual_rmsnorm (bit-identical to it with a = NULL), xh optional f16 copy of xn, and the router
+ * logits of xn into logits, as phase 1 of hmoe_moe_decode_layer computes them; run hmoe_moe_decode_layer on xn with
+ * the same logits and phases 14 to finish the layer. Passing y = h to that call adds the layer's output into the
+ * residual (the combine of runtime/tier/cn.cu:48-103), so a decode stack needs one norm + router launch per layer. */
+int hmoe_norm_router(const float* h, const float* norm_w, float eps, int R, const float* wt, int E, float* logits,
+                     uint16_t* xn, void* xh, void* stream);
 
 #ifdef __cplusplus
 }

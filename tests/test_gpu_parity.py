@@ -246,7 +246,7 @@ def test_stack_layers_and_graph(dev):
     x = synth.gen_x(4, R, dev)
     st.x.copy_(x)
     tr = []
-    h_eager = st.step(trace=tr).clone()
+    h_eager = st.step(trace=tr, fused=False).clone()
     torch.cuda.synchronize()
     h_prev = x.float().cpu().numpy()
     y_prev = None
@@ -268,6 +268,71 @@ def test_stack_layers_and_graph(dev):
         st.replay()
         torch.cuda.synchronize()
         assert torch.equal(st.h, h_eager), f"replay {rep} differs from the eager step"
+        junk = torch.randn(1 << 20, device=dev).sum()           # eager work between replays
+        torch.cuda.synchronize()
+    del st, layers
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("R", [1, 4, 16])
+def test_norm_router_bit_identical(dev, R):
+    """the fused RMSNorm + router launch against the residual + RMSNorm kernel followed by the router: xn, its f16 copy
+    and the logits bit-identical (the reference's own criterion for its fused norm, nr4_kernel.cuh:4-9), xn also
+    against the oracle's norm"""
+    log(f"norm_router R={R}")
+    lay = gpu_layer("c0", dev, layer=0)
+    g = torch.Generator().manual_seed(R)
+    h = (torch.randn((R, H), generator=g) * 3.0).to(dev)
+    w = (1.0 + 0.02 * torch.randn(H, generator=g)).to(dev)
+    xn_a = torch.empty((R, H), dtype=torch.bfloat16, device=dev)
+    xh_a = torch.empty((R, H), dtype=torch.float16, device=dev)
+    call("hmoe_residual_rmsnorm", ptr(h.clone()), None, ptr(w), R, 1e-5, ptr(xn_a), ptr(xh_a),
+         torch.cuda.current_stream().cuda_stream)
+    lg_a, ctr = router.buffers(R, dev)
+    sel = torch.empty((R, 8), dtype=torch.int64, device=dev); rw = torch.empty((R, 8), dtype=torch.float16, device=dev)
+    router.router_fused(xn_a, lay.wg, lay.bias, lg_a, ctr, sel, rw, 8, 2.5)
+    xn_b = torch.empty_like(xn_a); xh_b = torch.empty_like(xh_a)
+    lg_b, _ = router.buffers(R, dev)
+    h_before = h.clone()
+    for _ in range(2):                                          # repeated calls on the same buffers
+        router.norm_router(h, w, 1e-5, lay.wg, lg_b, xn_b, xh_b)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h_before)
+    assert np.array_equal(u16(xn_a), u16(xn_b)) and np.array_equal(u16(xh_a), u16(xh_b))
+    E = lay.wg.shape[0]
+    la = lg_a[:R * 256].view(R, 256)[:, :E].cpu().numpy().view(np.uint32)
+    lb = lg_b[:R * 256].view(R, 256)[:, :E].cpu().numpy().view(np.uint32)
+    assert np.array_equal(la, lb)
+    _, xn_ref = O.residual_rmsnorm(h_before.cpu().numpy(), None, w.cpu().numpy(), 1e-5)
+    assert np.array_equal(u16(xn_b), xn_ref)
+
+
+@pytest.mark.parametrize("R", [1, 4, 16])
+def test_stack_fused_matches_unfused(dev, R):
+    """the decode stack with the fused norm + router launch and the layer output added into the residual gives the
+    bits of the unfused stack (norm kernel, router inside the decode layer, combine), layer by layer, and its captured
+    graph replays them"""
+    log(f"fused stack R={R}")
+    _LAYERS.clear()
+    torch.cuda.empty_cache()
+    layers = [synth.make_layer(l, dev) for l in range(2)]
+    ws = [synth.gen_normal(synth.key(synth.SEED, l, synth.KIND["NORM_W"]), H, dev, 1.0, 0.02) for l in range(2)]
+    st = DecodeStack(layers, ws, R)
+    st.x.copy_(synth.gen_x(40 + R, R, dev))
+    tu, tf = [], []
+    h_u = st.step(trace=tu, fused=False).clone()
+    h_f = st.step(trace=tf, fused=True).clone()
+    torch.cuda.synchronize()
+    for l in range(2):
+        assert torch.equal(tu[l][0], tf[l][0]), f"layer {l}: residual"
+        assert torch.equal(tu[l][1], tf[l][1]), f"layer {l}: xn"
+        assert torch.equal(tu[l][3], tf[l][3]) and torch.equal(tu[l][4], tf[l][4]), f"layer {l}: routing"
+    assert torch.equal(h_u, h_f)
+    st.capture(fused=True)
+    for rep in range(3):
+        st.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(st.h, h_f), f"replay {rep}"
         junk = torch.randn(1 << 20, device=dev).sum()           # eager work between replays
         torch.cuda.synchronize()
     del st, layers
