@@ -466,6 +466,26 @@ __global__ void __launch_bounds__(DW * 64) dn6_kernel(
     };
     DnItem A, B;
     load(A, 0);                                                 // (unconditional: a stand-in tile when nr == 0)
+    // the act rows of quad qd for this wave's slot and k quarter, loaded with no select after them (a select would
+    // wait for the loads where it stands): rows past R read row 0 (their outputs are never stored), a slot past m
+    // reads slot m - 1 and its wave's partial is zeroed
+    // (buffer loads: the slot offset is scalar and the lane's offset one 32-bit register, where a 64-bit lane address
+    // would not fit the register budget)
+    f16x8 xa[16];
+    const __amdgpu_buffer_rsrc_t act_rs = __builtin_amdgcn_make_buffer_rsrc((void*) act, (short) 0,
+                                                                           (int) (ACT_SLOTS * MAXR * I * 2), 0x00020000);
+    auto load_act = [&](int qd) {
+        const int j = __builtin_amdgcn_readfirstlane(min(4 * qd + sw, max(m - 1, 0)));
+        // the lane's byte offset in a slot, formed here from an opaque copy of the thread index so that it is not
+        // kept in a register across the loop (the loop has none to spare)
+        int tid;
+        asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int) threadIdx.x));
+        const int tl = tid & 15, act_lane = ((tl < R ? tl : 0) * I + 512 * ((tid >> 6) & 3) + 8 * ((tid >> 4) & 3)) * 2;
+        #pragma unroll
+        for (int t = 0; t < 16; ++t)
+            xa[t] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(act_rs, act_lane + 64 * t,
+                                                                                    j * MAXR * I * 2, 0));
+    };
     if (SH)
     {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -480,36 +500,27 @@ __global__ void __launch_bounds__(DW * 64) dn6_kernel(
             reduce(acc, 1, 0, b + G);
         }
     }
-    int cur_q = -1;
-    f16x8 xa[16];
+    load_act(r0 / NB_H);
     auto run = [&](const DnItem& S, int i, int par) {
         const int it = r0 + i, qd = it / NB_H, nb = it - qd * NB_H;
-        if (qd != cur_q)
-        {
-            // the quad's act rows for this wave's slot and k quarter (zero for a slot past m)
-            cur_q = qd;
-            const int j = 4 * qd + sw;
-            const bool use = live && j < m;
-            const _Float16* ar = act + ((size_t) min(j, m - 1) * MAXR + (live ? tok : 0)) * I + 512 * kq + 8 * ks;
-            #pragma unroll
-            for (int t = 0; t < 16; ++t)
-            {
-                const u32x4 v = ld16(ar + 32 * t);
-                xa[t] = use ? as_f16x8(v) : (f16x8) {};
-            }
-        }
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         #pragma unroll
         for (int k = 0; k < 4; ++k) group_i4(xa + 4 * k, S.d[k], scale_of(S.s, k), acc, dq);
+        if (4 * qd + sw >= m) acc = (f32x4) {0.f, 0.f, 0.f, 0.f};     // a slot past m adds nothing
+        // the next item's act when it opens a new quad: issued after this item's MFMAs and before the next prefetch,
+        // so waiting for it does not wait for that prefetch as well
+        if (i + 1 < nr && it + 1 == (qd + 1) * NB_H) load_act(qd + 1);
         reduce(acc, par, part0 + qd, nb);
     };
     const int p0 = s_mine & 1;                                  // red parity of the first routed item
     for (int i = 0; i < nr; i += 2)
     {
         load(B, i + 1);
+        __builtin_amdgcn_sched_barrier(0);                      // the prefetch goes out before this item's MFMAs
         run(A, i, p0);
         if (i + 1 >= nr) break;
         load(A, i + 2);
+        __builtin_amdgcn_sched_barrier(0);
         run(B, i + 1, p0 ^ 1);
     }
 }
