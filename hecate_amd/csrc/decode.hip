@@ -166,7 +166,8 @@ __global__ void __launch_bounds__(GW * 64) gu7_kernel(
     const bool live = tok < R;
     // Loads are issued in the order they are consumed (the wait counter is in order) and unconditionally (a load
     // under a branch makes the compiler wait for every outstanding load where the paths meet): x, the window's
-    // pointer tables (x standing in without a window), the logits of the wave's rows, then the shared units.
+    // pointer tables (x standing in without a window), the given picks, the logits of the wave's rows, then the
+    // shared units.
     const uint16_t* xr = (const uint16_t*) x + (size_t) (live ? tok : 0) * H + 512 * w + 8 * ks;
     u32x4 raw[16];
     #pragma unroll
@@ -176,6 +177,9 @@ __global__ void __launch_bounds__(GW * 64) gu7_kernel(
     const int64_t* xt = (const int64_t*) x;
     const int64_t t0 = ldg<int64_t>(hot ? gate_w + te : xt), t1 = ldg<int64_t>(hot ? up_w + te : xt);
     const int64_t t2 = ldg<int64_t>(hot ? gate_s + te : xt), t3 = ldg<int64_t>(hot ? up_s + te : xt);
+    // the given picks (used without logits; with logits sel / rw are the output buffers, read and ignored)
+    const int pi = min((int) threadIdx.x, R * TOPK - 1);
+    const Pick pk = {ldg<int64_t>(sel + pi), ldg<uint16_t>(rw + pi)};
     RowIn r0, r1;                                              // rows w and w + GW (one bias)
     if (logits)
     {
@@ -222,7 +226,7 @@ __global__ void __launch_bounds__(GW * 64) gu7_kernel(
         if (b == 0 && threadIdx.x < R * TOPK) { sel[threadIdx.x] = ssel[threadIdx.x]; rw[threadIdx.x] = srw[threadIdx.x]; }
         route(ssel, srw, R, lo, n_hot, rt);
     }
-    else route(sel, rw, R, lo, n_hot, rt);
+    else route_picks(pk, R, lo, n_hot, rt);
     const int m = rt.m;
     if (threadIdx.x < m)
     {
