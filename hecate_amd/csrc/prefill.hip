@@ -260,15 +260,19 @@ __global__ void __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(2))) pg
                     #pragma unroll
                     for (int m = 0; m < NMAT; ++m)
                         a[st][m] = DENSE ? as_f16x8(ring[s].q[st][m][k]) : dq8s(ring[s].q[st][m][0][k], sh[st][m], dq);
+                // the k step's input tiles read together (tiles past the block read stale LDS data, never used), so
+                // the LDS latency is paid once per k step rather than once per tile
+                f16x8 bvs[8];
+                #pragma unroll
+                for (int tt = 0; tt < 8; ++tt) bvs[tt] = as_f16x8(cur[(tt * 4 + k) * 64 + l]);
                 #pragma unroll
                 for (int tt = 0; tt < 8; ++tt)
                 {
                     if (tt >= ntt) break;
-                    const f16x8 bv = as_f16x8(cur[(tt * 4 + k) * 64 + l]);
                     #pragma unroll
                     for (int st = 0; st < NS; ++st)
                         #pragma unroll
-                        for (int m = 0; m < NMAT; ++m) acc[st][m][tt] = mfma16(a[st][m], bv, acc[st][m][tt]);
+                        for (int m = 0; m < NMAT; ++m) acc[st][m][tt] = mfma16(a[st][m], bvs[tt], acc[st][m][tt]);
                 }
             }
             fetch(min(kg + D, KG - 1), sc);                 // refill the slot just used (clamped at the end)
