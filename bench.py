@@ -7,7 +7,8 @@ Headline (`value`): the 16-row decode step (8 requests + 8 draft rows, Zipf(1.1)
 (router + routed int4 experts + shared expert + bf16 output) per step, in tokens/s. Steps cycle over 6 seeded
 layers and 64 seeded inputs so consecutive steps stream different weights (the working set of a step is far above
 the 256 MB last-level cache, as in a real decode pass through 75+ layers). Extras: decode at 1 and 8 rows, the
-2048-token prefill chunk, the 176-resident partial tier at 1/4/8 rows and the 16-layer hipGraph step at 4 rows.
+2048-token prefill chunk, the 176-resident partial tier at 1/4/8 rows, the same split with the other 80 experts on the
+host-CPU tier, and the 16-layer hipGraph step at 4 rows.
 One JSON line on stdout; progress on stderr.
 """
 import argparse
@@ -163,6 +164,38 @@ def partial_workload(torch, synth, steps, warmup, dev, n_layers=4):
     return out
 
 
+def tiered_workload(torch, synth, steps, warmup, dev, threads=8):
+    """config 3 with the other 80 experts on the host-CPU tier (tier_split.py's split): route on the GPU, hand the
+    rows to the pool through the device-mapped mailbox, run the 176 resident experts into the fp32 partial
+    meanwhile, then add the pool's partial on the same stream; one layer, 32 seeded inputs per row count"""
+    import numpy as np
+    from hecate_amd.cpu_tier import CpuTier, decode_split, host_experts
+    lay = synth.make_layer(0, dev, resident=synth.popularity_order()[:176], shared=False)
+    cpu = CpuTier(threads=threads)
+    out = {"cpu_threads": threads}
+    try:
+        cpu.add_layer(0, 176, host_experts(0, lay.perm[176:], dev))
+        for R in (1, 4, 8):
+            xs = [synth.gen_x(3500 + 16 * R + i, R, dev) for i in range(32)]
+            part = synth.gen_normal(synth.key(synth.SEED, 0, synth.KIND["PARTIAL"], R), R * H, dev, 0.0,
+                                    0.1).view(R, H)
+            el = timed(torch, lambda i: decode_split(lay, cpu, 0, xs[i % 32], part), steps, warmup)
+            el_gpu = timed(torch, lambda i: (lay.route(xs[i % 32]), lay.experts_decode(R, part, False)), steps, warmup)
+            cold = []
+            for i in range(32):
+                sel, _ = lay.route(xs[i])
+                cold.append(len(torch.unique(sel[sel >= 176])))
+            out[f"B{R}"] = {"us_per_step": el / steps * 1e6, "us_per_token": el / steps * 1e6 / R,
+                            "gpu_tier_alone_us_per_step": el_gpu / steps * 1e6,
+                            "cpu_experts_per_step_mean": float(np.mean(cold))}
+    finally:
+        torch.cuda.synchronize()
+        cpu.close()
+    del lay
+    torch.cuda.empty_cache()
+    return out
+
+
 def graph_workload(torch, synth, steps, warmup, dev, n_layers=16, R=4):
     import numpy as np
     from hecate_amd.stack import DecodeStack
@@ -253,7 +286,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None, choices=[None, "decode16", "decode1", "decode8", "prefill", "partial",
-                                                     "graph16", "copy"])
+                                                     "graph16", "copy", "tiered"])
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the path would shard by "
@@ -284,6 +317,9 @@ def main():
     if only in (None, "graph16"):
         extra["graph_16_layers_b4"] = graph_workload(torch, synth, max(20, K // 4), max(3, W // 4), dev)
         log(f"[bench] graph16: {json.dumps(extra['graph_16_layers_b4'])}")
+    if only in (None, "tiered"):
+        extra["tiered_176_cpu80"] = tiered_workload(torch, synth, max(20, K // 10), max(3, W // 4), dev)
+        log(f"[bench] tiered: {json.dumps(extra['tiered_176_cpu80'])}")
     if only == "copy":
         extra["copy_1gib"] = copy_workload(torch, max(10, K // 10), 3, dev)
     if head is None:

@@ -40,6 +40,14 @@ SIGNATURES = {
                                  P, P, P, i32, P]),
     "hmoe_residual_rmsnorm": (i32, [P, P, P, i32, f32, P, P, P]),
     "hmoe_norm_router": (i32, [P, P, f32, i32, P, i32, P, P, P, P]),
+    "hmoe_cpu_start": (i32, [P, i32, i32]),
+    "hmoe_cpu_add_layer": (i32, [i32, i32, i32, P, P]),
+    "hmoe_cpu_stats": (i32, [P, P]),
+    "hmoe_cpu_stop": (i32, []),
+    "hmoe_cpu_submit": (i32, [P, P, P, P, i32, i32, P]),
+    "hmoe_cpu_collect": (i32, [P, P, i32, P]),
+    "hmoe_cpu_mailbox_alloc": (i32, [P]),
+    "hmoe_cpu_mailbox_free": (i32, [P]),
 }
 
 

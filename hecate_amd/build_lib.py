@@ -12,7 +12,13 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libhecate_moe.so")
-SOURCES = ["common.hip", "decode.hip", "router.hip", "prefill.hip"]
+SOURCES = ["common.hip", "decode.hip", "router.hip", "prefill.hip", "cputier_gpu.hip"]
+HOST_SOURCES = ["cputier.cpp"]                 # host-only C++ (the CPU expert tier), built with the host compiler
+CXX = os.environ.get("CXX_HOST", "g++")
+# AVX2 / FMA / F16C is the x86-64-v3 level (every AVX2 EPYC and Xeon); no fp contraction, so the q8_0 arithmetic
+# rounds exactly as written
+HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-mavx2", "-mfma", "-mf16c", "-ffp-contract=off", "-pthread", "-Wall",
+              f"-I{os.path.join(ROOT, 'include')}"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("HMOE_ARCH", "gfx950")
 FLAGS = [
@@ -34,15 +40,25 @@ def _compile(src):
     return obj, err
 
 
+def _compile_host(src):
+    obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
+    cmd = [CXX] + HOST_FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"{CXX} failed on {src}:\n{r.stdout}{r.stderr}")
+    return obj, r.stdout + r.stderr
+
+
 def build(verbose=False):
     os.makedirs(OBJ, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(4, len(SOURCES))) as ex:
-        results = list(ex.map(_compile, SOURCES))
+    with ThreadPoolExecutor(max_workers=min(4, len(SOURCES) + len(HOST_SOURCES))) as ex:
+        jobs = [ex.submit(_compile, s) for s in SOURCES] + [ex.submit(_compile_host, s) for s in HOST_SOURCES]
+        results = [j.result() for j in jobs]
     for _, err in results:
         if err.strip() and verbose:
             print(err, file=sys.stderr)
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + [o for o, _ in results]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + [o for o, _ in results] + ["-lpthread"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")

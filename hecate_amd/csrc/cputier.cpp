@@ -1,0 +1,351 @@
+// cputier.cpp - the host-CPU expert tier (runtime/tier/cpuband.cpp: the Grace band) for x86 hosts: a persistent
+// pool of threads that serves decode jobs (<= 8 rows) from a mailbox in pinned, device-mapped host memory, runs the
+// cold experts (ids in [lo, lo + n)) with q8_0 activations and int4 x int8 dot products, and leaves an fp32 partial
+// for the GPU to add (the GPU side of the hand-off is in cputier_gpu.hip).
+//
+// Arithmetic, as cpuband.cpp with group-128 bf16 scales:
+//   * picks in first appearance over rows, then top-k order; wgt[p][r] = sum of the f16 routing weights (:151-178);
+//   * x rows and each pick's activation quantised per 32: s = absmax / 127 (1 if 0), q = lrintf(v / s) (:106-111);
+//   * y[n] over groups g of 128: four fp32 lanes accumulate float(dot) * xs per 32-block (lane i takes the products
+//     of k + 4i..+4 and k + 16 + 4i..+4), fold (a0 + a1) + (a2 + a3), y = fma(s[n][g], fold, y) (:80-104);
+//   * act = g / (1 + expf(-g)) * u * wgt, then q8_0 (:201-207);
+//   * out[r][n] = sum over picks in pick order of the down rows, from 0 (:210-218).
+// Threads split the output rows of every GEMV; a job is a fixed sequence of barriers, so results do not depend on
+// the thread count.
+#include "hecate_moe.h"
+
+#include <atomic>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <immintrin.h>
+#include <mutex>
+#include <sched.h>
+#include <thread>
+#include <vector>
+
+namespace hmoe_cpu {
+
+constexpr int H = HMOE_H, I = HMOE_I, TOPK = HMOE_TOPK;
+constexpr int CMAXR = HMOE_CPU_MAXR;
+
+static inline float bf2f(uint16_t b) { uint32_t u = (uint32_t) b << 16; float f; std::memcpy(&f, &u, 4); return f; }
+static inline float h2f(uint16_t h) { return (float) _cvtsh_ss(h); }
+
+// one expert matrix on the host: codes [N][K / 2] (row-major, low nibble first), bf16 scales [N][K / 128]
+struct Mat { const uint8_t* q = nullptr; const uint16_t* s = nullptr; };
+struct Expert { Mat gate, up, down; };
+struct Layer { int lo = 0; std::vector<Expert> ex; };
+
+// the job's work arrays (sized for CMAXR rows and up to CMAXR * TOPK picks)
+struct Work
+{
+    int P = 0, R = 0;
+    int32_t pick[CMAXR * TOPK];
+    float wgt[CMAXR * TOPK][CMAXR];
+    int nrows[CMAXR * TOPK], rows[CMAXR * TOPK][CMAXR];
+    std::vector<int8_t> xq;        // [R][H]
+    std::vector<float> xs;         // [R][H / 32]
+    std::vector<float> gy, uy;     // [R][I] of the current pick
+    std::vector<int8_t> aq;        // [P][R][I]
+    std::vector<float> as;         // [P][R][I / 32]
+    Work() : xq(CMAXR * H), xs(CMAXR * H / 32), gy(CMAXR * I), uy(CMAXR * I), aq((size_t) CMAXR * TOPK * CMAXR * I),
+             as((size_t) CMAXR * TOPK * CMAXR * I / 32) {}
+};
+
+struct Pool
+{
+    std::vector<std::thread> th;
+    std::vector<Layer> layers;
+    hmoe_cpu_mailbox* mb = nullptr;
+    std::atomic<int> stop{0};
+    std::atomic<int> bar_count{0}, bar_gen{0};
+    int nthr = 0;
+    Work w;
+    std::atomic<long long> jobs{0}, picks{0};
+};
+
+static Pool* g_pool = nullptr;
+static std::mutex g_mu;
+
+// barrier for the pool's threads (sense by generation)
+static void barrier(Pool& p)
+{
+    const int gen = p.bar_gen.load(std::memory_order_acquire);
+    if (p.bar_count.fetch_add(1, std::memory_order_acq_rel) + 1 == p.nthr)
+    {
+        p.bar_count.store(0, std::memory_order_relaxed);
+        p.bar_gen.store(gen + 1, std::memory_order_release);
+    }
+    else
+        while (p.bar_gen.load(std::memory_order_acquire) == gen) _mm_pause();
+}
+
+// q8_0 of a 32-element group
+static void quant_group(const float* v, int8_t* q, float* sc)
+{
+    float m = 0.0f;
+    for (int k = 0; k < 32; ++k) m = std::fmax(m, std::fabs(v[k]));
+    const float s = m > 0 ? m / 127.0f : 1.0f;
+    *sc = s;
+    const float inv = 1.0f / s;
+    for (int k = 0; k < 32; ++k) q[k] = (int8_t) lrintf(v[k] * inv);
+}
+
+// the four lane sums of one 32-block: lane i = sum of z * x over k 4i..4i+3 and 16 + 4i..16 + 4i + 3
+static inline __m128i block_dot(__m256i z, const int8_t* x)
+{
+    const __m256i xv = _mm256_loadu_si256((const __m256i*) x);
+    // |z| (u8) times x with z's sign, summed in pairs (int16), then in fours (int32)
+    const __m256i pr = _mm256_maddubs_epi16(_mm256_sign_epi8(z, z), _mm256_sign_epi8(xv, z));
+    const __m256i q4 = _mm256_madd_epi16(pr, _mm256_set1_epi16(1));       // sums of k 4m..4m+3, m = 0..7
+    return _mm_add_epi32(_mm256_castsi256_si128(q4), _mm256_extracti128_si256(q4, 1));
+}
+
+// rows [n0, n1) of y[r][n] = W x[r] for nr rows (xq [nr][K], xs [nr][K / 32]), y row stride ys
+static void gemv(const Mat& m, int K, const int8_t* xq, const float* xs, int nr, int n0, int n1, float* y, int ys)
+{
+    const __m256i lo4 = _mm256_set1_epi8(0x0f), eight = _mm256_set1_epi8(8);
+    for (int n = n0; n < n1; ++n)
+    {
+        const uint8_t* qr = m.q + (size_t) n * (K / 2);
+        const uint16_t* sr = m.s + (size_t) n * (K / 128);
+        float yr[CMAXR];
+        for (int r = 0; r < nr; ++r) yr[r] = 0.0f;
+        for (int g = 0; g < K / 128; ++g)
+        {
+            __m128 acc[CMAXR];
+            for (int r = 0; r < nr; ++r) acc[r] = _mm_setzero_ps();
+            for (int b = 0; b < 4; ++b)
+            {
+                const int k = g * 128 + b * 32;
+                // the block's 32 codes in k order, minus 8: byte j = code(k + 2j) | code(k + 2j + 1) << 4
+                const __m128i raw = _mm_loadu_si128((const __m128i*) (qr + k / 2));
+                const __m128i lo = _mm_and_si128(raw, _mm256_castsi256_si128(lo4));
+                const __m128i hi = _mm_and_si128(_mm_srli_epi16(raw, 4), _mm256_castsi256_si128(lo4));
+                const __m256i z = _mm256_sub_epi8(
+                    _mm256_set_m128i(_mm_unpackhi_epi8(lo, hi), _mm_unpacklo_epi8(lo, hi)), eight);
+                for (int r = 0; r < nr; ++r)
+                {
+                    const __m128 d = _mm_cvtepi32_ps(block_dot(z, xq + (size_t) r * K + k));
+                    acc[r] = _mm_fmadd_ps(d, _mm_set1_ps(xs[(size_t) r * (K / 32) + k / 32]), acc[r]);
+                }
+            }
+            const float sc = bf2f(sr[g]);
+            for (int r = 0; r < nr; ++r)
+            {
+                alignas(16) float a[4];
+                _mm_store_ps(a, acc[r]);
+                yr[r] = std::fma(sc, (a[0] + a[1]) + (a[2] + a[3]), yr[r]);
+            }
+        }
+        for (int r = 0; r < nr; ++r) y[(size_t) r * ys + n] = yr[r];
+    }
+}
+
+static void range(int total, int t, int T, int& a, int& b)
+{
+    a = (int) ((long long) total * t / T);
+    b = (int) ((long long) total * (t + 1) / T);
+}
+
+// one job, by every thread of the pool (t = 0 .. nthr - 1)
+static void run_job(Pool& p, int t)
+{
+    hmoe_cpu_mailbox* mb = p.mb;
+    Work& w = p.w;
+    const int T = p.nthr;
+    if (t == 0)
+    {
+        const int R = mb->rows, L = mb->layer;
+        w.R = (R >= 1 && R <= CMAXR) ? R : 0;
+        w.P = 0;
+        if (w.R && L >= 0 && L < (int) p.layers.size())
+        {
+            const Layer& ly = p.layers[L];
+            const int n = (int) ly.ex.size();
+            for (int i = 0; i < w.R * TOPK; ++i)
+            {
+                const int64_t e = mb->sel[i] - ly.lo;
+                if (e < 0 || e >= n) continue;
+                int j = 0;
+                while (j < w.P && w.pick[j] != (int32_t) e) ++j;
+                if (j == w.P) { w.pick[w.P] = (int32_t) e; for (int r = 0; r < w.R; ++r) w.wgt[w.P][r] = 0.0f; ++w.P; }
+                w.wgt[j][i / TOPK] += h2f(mb->rw[i]);
+            }
+            for (int q = 0; q < w.P; ++q)
+            {
+                int nr = 0;
+                for (int r = 0; r < w.R; ++r) if (w.wgt[q][r] != 0.0f) w.rows[q][nr++] = r;
+                w.nrows[q] = nr;
+            }
+        }
+    }
+    barrier(p);
+    const int R = w.R, P = w.P;
+    const Layer* ly = (R && mb->layer >= 0 && mb->layer < (int) p.layers.size()) ? &p.layers[mb->layer] : nullptr;
+    // q8_0 of every row of x
+    {
+        int a, b;
+        range(R * H / 32, t, T, a, b);
+        for (int gi = a; gi < b; ++gi)
+        {
+            float v[32];
+            for (int k = 0; k < 32; ++k) v[k] = bf2f(mb->x[(size_t) gi * 32 + k]);
+            quant_group(v, w.xq.data() + (size_t) gi * 32, w.xs.data() + gi);
+        }
+    }
+    barrier(p);
+    // per pick: gate / up over the pick's rows, then act -> q8_0
+    static thread_local std::vector<int8_t> xqp(CMAXR * H);
+    static thread_local std::vector<float> xsp(CMAXR * H / 32);
+    for (int q = 0; q < P; ++q)
+    {
+        const Expert& ex = ly->ex[w.pick[q]];
+        const int nr = w.nrows[q];
+        for (int j = 0; j < nr; ++j)
+        {
+            const int r = w.rows[q][j];
+            std::memcpy(xqp.data() + (size_t) j * H, w.xq.data() + (size_t) r * H, H);
+            std::memcpy(xsp.data() + (size_t) j * (H / 32), w.xs.data() + (size_t) r * (H / 32), sizeof(float) * (H / 32));
+        }
+        int a, b;
+        range(I, t, T, a, b);
+        gemv(ex.gate, H, xqp.data(), xsp.data(), nr, a, b, w.gy.data(), I);
+        gemv(ex.up, H, xqp.data(), xsp.data(), nr, a, b, w.uy.data(), I);
+        barrier(p);
+        range(nr * I / 32, t, T, a, b);
+        for (int gi = a; gi < b; ++gi)
+        {
+            const int j = gi / (I / 32), k0 = (gi % (I / 32)) * 32;
+            const float wt = w.wgt[q][w.rows[q][j]];
+            float v[32];
+            for (int k = 0; k < 32; ++k)
+            {
+                const float gg = w.gy[(size_t) j * I + k0 + k];
+                v[k] = gg / (1.0f + expf(-gg)) * w.uy[(size_t) j * I + k0 + k] * wt;
+            }
+            quant_group(v, w.aq.data() + ((size_t) q * CMAXR + j) * I + k0,
+                        w.as.data() + (((size_t) q * CMAXR + j) * I + k0) / 32);
+        }
+        barrier(p);
+    }
+    // down: output rows split over the threads, picks in order, summed into out from 0
+    {
+        int a, b;
+        range(H, t, T, a, b);
+        for (int r = 0; r < R; ++r) std::memset(mb->out + (size_t) r * H + a, 0, sizeof(float) * (size_t) (b - a));
+        static thread_local std::vector<float> y1(CMAXR * H);
+        for (int q = 0; q < P; ++q)
+        {
+            const Expert& ex = ly->ex[w.pick[q]];
+            const int nr = w.nrows[q];
+            gemv(ex.down, I, w.aq.data() + (size_t) q * CMAXR * I, w.as.data() + (size_t) q * CMAXR * I / 32, nr, a, b,
+                 y1.data(), H);
+            for (int j = 0; j < nr; ++j)
+            {
+                float* o = mb->out + (size_t) w.rows[q][j] * H;
+                for (int n = a; n < b; ++n) o[n] += y1[(size_t) j * H + n];
+            }
+        }
+    }
+    barrier(p);
+    if (t == 0)
+    {
+        p.jobs.fetch_add(1, std::memory_order_relaxed);
+        p.picks.fetch_add(P, std::memory_order_relaxed);
+        mb->err = !R ? 1 : (ly ? 0 : 2);                   // 1: bad row count, 2: no such layer
+        __atomic_store_n(&mb->pending, 0, __ATOMIC_RELEASE);
+    }
+}
+
+static void worker(Pool* p, int t, int core)
+{
+    if (core >= 0)
+    {
+        cpu_set_t cs;
+        CPU_ZERO(&cs);
+        CPU_SET(core, &cs);
+        sched_setaffinity(0, sizeof(cs), &cs);       // best effort
+    }
+    int idle = 0;
+    while (true)
+    {
+        // every thread watches the flag; all see the same job because the flag is cleared only after the job's last
+        // barrier, which every thread passes
+        if (p->stop.load(std::memory_order_acquire)) return;
+        if (__atomic_load_n(&p->mb->pending, __ATOMIC_ACQUIRE) == 1)
+        {
+            idle = 0;
+            run_job(*p, t);
+            // wait until thread 0 has cleared the flag before looking for the next job
+            while (__atomic_load_n(&p->mb->pending, __ATOMIC_ACQUIRE) == 1 && !p->stop.load(std::memory_order_acquire))
+                _mm_pause();
+            continue;
+        }
+        if (++idle < 4096) _mm_pause();
+        else std::this_thread::yield();
+    }
+}
+
+}  // namespace hmoe_cpu
+
+namespace hmoe { int set_error(int code, const char* fmt, ...); }    // the library's error record (hmoe_last_error)
+
+using namespace hmoe_cpu;
+
+extern "C" int hmoe_cpu_start(hmoe_cpu_mailbox* mb, int threads, int first_core)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_pool) return hmoe::set_error(HMOE_ERR_ARG, "cpu_start: the pool is running");
+    if (!mb || threads < 1 || threads > 256) return hmoe::set_error(HMOE_ERR_ARG, "cpu_start: mailbox / threads");
+    Pool* p = new Pool();
+    p->mb = mb;
+    p->nthr = threads;
+    mb->pending = 0;
+    g_pool = p;
+    for (int t = 0; t < threads; ++t) p->th.emplace_back(worker, p, t, first_core >= 0 ? first_core + t : -1);
+    return 0;
+}
+
+extern "C" int hmoe_cpu_add_layer(int layer, int lo, int n, const uint8_t* const* q, const uint16_t* const* s)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_pool) return hmoe::set_error(HMOE_ERR_ARG, "cpu_add_layer: no pool");
+    if (layer < 0 || layer > 4096 || lo < 0 || n < 0 || n > 256 || (n && (!q || !s))) return hmoe::set_error(HMOE_ERR_ARG, "cpu_add_layer: arguments");
+    if (__atomic_load_n(&g_pool->mb->pending, __ATOMIC_ACQUIRE)) return hmoe::set_error(HMOE_ERR_ARG, "cpu_add_layer: a job is in flight");
+    if ((int) g_pool->layers.size() <= layer) g_pool->layers.resize(layer + 1);
+    Layer& L = g_pool->layers[layer];
+    L.lo = lo;
+    L.ex.assign(n, Expert{});
+    for (int e = 0; e < n; ++e)
+    {
+        // q / s: per expert the gate, up and down pointers (3 n each)
+        L.ex[e].gate = {q[3 * e + 0], s[3 * e + 0]};
+        L.ex[e].up = {q[3 * e + 1], s[3 * e + 1]};
+        L.ex[e].down = {q[3 * e + 2], s[3 * e + 2]};
+        for (int k = 0; k < 3; ++k)
+            if (!q[3 * e + k] || !s[3 * e + k]) return hmoe::set_error(HMOE_ERR_ARG, "cpu_add_layer: null matrix");
+    }
+    return 0;
+}
+
+extern "C" int hmoe_cpu_stats(long long* jobs, long long* picks)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_pool) return hmoe::set_error(HMOE_ERR_ARG, "cpu_stats: no pool");
+    if (jobs) *jobs = g_pool->jobs.load();
+    if (picks) *picks = g_pool->picks.load();
+    return 0;
+}
+
+extern "C" int hmoe_cpu_stop(void)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_pool) return 0;
+    g_pool->stop.store(1, std::memory_order_release);
+    for (auto& t : g_pool->th) t.join();
+    delete g_pool;
+    g_pool = nullptr;
+    return 0;
+}

@@ -168,6 +168,51 @@ int hmoe_residual_rmsnorm(float* r, float* a, const float* w, int R, float eps, 
 int hmoe_norm_router(const float* h, const float* norm_w, float eps, int R, const float* wt, int E, float* logits,
                      uint16_t* xn, void* xh, void* stream);
 
+/* ---- host-CPU expert tier: runtime/tier/cpuband.cpp (cb_start :241, cb_add_layer :228, cb_stats :254, cb_stop :256,
+ * the job of worker :113-223) for x86 hosts ----
+ * A pool of host threads serves decode jobs of <= HMOE_CPU_MAXR rows from a mailbox: the cold experts of the job's
+ * layer (ids in [lo, lo + n)) with q8_0 activations and int4 x int8 dot products (the arithmetic of cpuband.cpp with
+ * bf16 group-128 scales), the fp32 partial into out. The mailbox is any host memory the pool can read; for the GPU
+ * hand-off it must be pinned and device-mapped (hipHostMalloc, mapped + coherent). Protocol: the poster fills rows,
+ * layer, sel, rw and x, then sets pending = 1 (release); the pool computes, writes out and err (0; 1 for a row count
+ * outside [1, 8], 2 for a layer it does not hold, with out zero), then sets pending = 0 (release). Jobs are
+ * serialised by the flag, so a job does not overlap the next. */
+#define HMOE_CPU_MAXR 8        /* rows per CPU job (cpuband.cpp:7, 154: MAXR = 8) */
+typedef struct hmoe_cpu_mailbox
+{
+    int32_t pending;                              /* 1 = a job is posted, 0 = done (own 128-byte line) */
+    int32_t pad0[31];
+    int32_t rows, layer, err;                     /* job header, written before pending */
+    int32_t gpu_err;                              /* sticky, set by the GPU side: 1 a collect's wait ran out (partial
+                                                     not added), 2 a hand-off found the pool busy (job not posted);
+                                                     the host reads and clears it */
+    int32_t pad1[28];
+    int64_t sel[HMOE_CPU_MAXR * HMOE_TOPK];       /* global expert ids [rows][8] */
+    uint16_t rw[HMOE_CPU_MAXR * HMOE_TOPK];       /* f16 routing weights [rows][8] */
+    uint16_t x[HMOE_CPU_MAXR * HMOE_H];           /* bf16 rows */
+    float out[HMOE_CPU_MAXR * HMOE_H];            /* fp32 partial [rows][H] */
+} hmoe_cpu_mailbox;
+/* start the pool (threads >= 1, pinned to cores first_core + t when first_core >= 0) on a mailbox; one pool per process */
+int hmoe_cpu_start(hmoe_cpu_mailbox* mb, int threads, int first_core);
+/* the cold experts of a layer, host memory: q[3 e + {0, 1, 2}] the row-major int4 codes (cpuband.cpp:3-4: [N][K/2],
+ * low nibble first) of gate [I][H], up [I][H], down [H][I] of cold expert e (id lo + e), s[...] their bf16 [N][K/128]
+ * scales; the pool keeps the pointers (the caller keeps the memory alive) */
+int hmoe_cpu_add_layer(int layer, int lo, int n, const uint8_t* const* q, const uint16_t* const* s);
+int hmoe_cpu_stats(long long* jobs, long long* picks);
+int hmoe_cpu_stop(void);
+/* the GPU side of a job, one kernel each, capturable in a hipGraph. hmoe_cpu_submit: x bf16 [R][H], sel, rw (device,
+ * 16-byte aligned) copied into the mailbox, rows / layer / err written, then pending = 1 with a system-scope release
+ * (runtime/tier/moe4/moe4.cu:719-738 moe4_handoff_kernel). hmoe_cpu_collect: waits for pending == 0 and adds out into
+ * y fp32 [R][H] (runtime/tier/tier_split.py:577-644 tier_combine, the graph form's spinning combine). Both waits are
+ * bounded (2 s of wall clock); past the bound the kernel sets gpu_err and returns. The mailbox must come from
+ * hmoe_cpu_mailbox_alloc (or be otherwise device-mapped). */
+int hmoe_cpu_submit(hmoe_cpu_mailbox* mb, const void* x, const int64_t* sel, const uint16_t* rw, int R, int layer,
+                    void* stream);
+int hmoe_cpu_collect(hmoe_cpu_mailbox* mb, float* y, int R, void* stream);
+/* a mapped, coherent pinned mailbox (hipHostMalloc) and its release */
+int hmoe_cpu_mailbox_alloc(hmoe_cpu_mailbox** mb);
+int hmoe_cpu_mailbox_free(hmoe_cpu_mailbox* mb);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,118 @@
+"""The host-CPU expert tier (hecate_amd/csrc/cputier.cpp) driven from the host through a plain-memory mailbox, as
+tools/dev/test_grace_picks.py drives cpuband's flags: bit-exact against the oracle's q8_0 mode (cpuband.cpp's
+arithmetic), a many-pick job equal to the sum of its one-pick jobs (test_grace_picks.py:95-152), the same bits for
+any thread count, and the error words of bad jobs. No GPU."""
+import numpy as np
+import pytest
+
+import pyoracle as O
+from hecate_amd.cpu_tier import CpuTier
+from hostref import HostLayer, x_rows
+
+LO, N = 248, 8                      # the cold window: ids 248..255 (local id = id - LO, as in a resident bank)
+
+
+@pytest.fixture(scope="module")
+def hl():
+    return HostLayer(0, shared=False)
+
+
+@pytest.fixture(scope="module")
+def cold(hl):
+    # the tier's local expert e is the host layer's local expert e (the window convention of the banks)
+    return [hl.expert(e) for e in range(N)]
+
+
+def start(cold, threads):
+    t = CpuTier(threads=threads, mapped=False)
+    t.add_layer(0, LO, cold)
+    return t
+
+
+def picks(R, seed):
+    """sel with 3 picks per row in the window (some shared between rows), the rest outside it; f16 weights"""
+    rng = np.random.default_rng(seed)
+    sel = np.stack([rng.choice(LO, 8, replace=False) for _ in range(R)]).astype(np.int64)
+    for r in range(R):
+        sel[r, rng.choice(8, 3, replace=False)] = LO + rng.choice(N, 3, replace=False)
+    rw = O.f32_to_f16((rng.random((R, 8)) * 0.5 + 0.05).astype(np.float32))
+    return sel, rw
+
+
+def oracle_q8(hl, x, sel, rw):
+    return O.moe(1, x, sel, rw, hl.table(sel, LO), LO, N, None, threads=8)
+
+
+@pytest.mark.parametrize("R", [1, 3, 8])
+def test_cpu_tier_matches_oracle_q8(hl, cold, R):
+    t = start(cold, 4)
+    try:
+        x = x_rows(500 + R, R)
+        sel, rw = picks(R, R)
+        t.post(x, sel, rw, 0)
+        out, err = t.wait()
+        assert err == 0
+        ref = oracle_q8(hl, x, sel, rw)
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+        assert t.stats()[0] == 1
+    finally:
+        t.close()
+
+
+def test_cpu_tier_job_is_sum_of_one_pick_jobs(hl, cold):
+    """a job with several cold picks equals the sum, in pick order from 0, of the jobs that keep one of them"""
+    t = start(cold, 4)
+    try:
+        R = 4
+        x = x_rows(77, R)
+        sel, rw = picks(R, 9)
+        t.post(x, sel, rw, 0)
+        full, _ = t.wait()
+        order = []                                   # pick order: first appearance over rows, then top-k
+        for e in sel.ravel():
+            if LO <= e < LO + N and e not in order:
+                order.append(int(e))
+        acc = np.zeros((R, 6144), np.float32)
+        for e in order:
+            s1 = np.where((sel >= LO) & (sel != e), 0, sel)      # the other cold picks moved out of the window
+            t.post(x, s1, rw, 0)
+            part, _ = t.wait()
+            acc = acc + part
+        assert np.array_equal(full.view(np.uint32), acc.view(np.uint32))
+    finally:
+        t.close()
+
+
+def test_cpu_tier_thread_count_does_not_change_bits(cold):
+    R = 5
+    x = x_rows(31, R)
+    sel, rw = picks(R, 4)
+    outs = []
+    for threads in (1, 3, 8):
+        t = start(cold, threads)
+        try:
+            t.post(x, sel, rw, 0)
+            outs.append(t.wait()[0])
+        finally:
+            t.close()
+    assert all(np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)) for o in outs[1:])
+
+
+def test_cpu_tier_bad_jobs(cold):
+    t = start(cold, 2)
+    try:
+        x = x_rows(3, 2)
+        sel, rw = picks(2, 1)
+        t.post(x, sel, rw, 5)                        # a layer the pool does not hold
+        out, err = t.wait()
+        assert err == 2 and not out.any()
+        t.post(x, sel, rw, 0)                        # and the pool still serves the next job
+        _, err = t.wait()
+        assert err == 0
+        t.mb.rows, t.mb.err = 9, 0                   # a row count past the mailbox
+        t.mb.pending = 1
+        t._rows = 1
+        _, err = t.wait()
+        assert err == 1
+    finally:
+        t.close()
