@@ -343,23 +343,35 @@ struct DnItem
 };
 
 constexpr int DN_GMIN = NB_H / 2, DN_GMAX = NB_H;   // grid range: one or two shared items per workgroup
+constexpr int XSH_LD = I + 8;                       // row stride (f16) of the down launch's shared act in LDS
+// the cost of a slot-quad change inside a workgroup's down range, in items (its act reload, 16 R KB, mostly from L2)
+#ifndef DN_XC_NUM
+#define DN_XC_NUM 4
+#endif
+#define DN_XCOST(R) (((R) * DN_XC_NUM) / 16)
 
 // workgroup b: (SH) shared items nb = b and b + G (when < NB_H), then a contiguous range of the routed items
 // (quad-major, so a quad's act stays in registers). Every item moves the same 64 KB; the ranges give every workgroup
 // floor or ceil of (shared + routed) / G items in total. The shared act, f16(silu(g) u), is formed here from the fp32
-// gate and up sums the gate/up launch left in the SHP_SLOT area of act.
-template <bool SH>
+// gate and up sums the gate/up launch left in the SHP_SLOT area of act, NJ float4 steps per thread (NJ * 4096
+// elements per workgroup cover the R live rows: the host picks the smallest of 1, 2, 4, 8 that does).
+template <bool SH, int NJ>
 __global__ void __launch_bounds__(DW * 64) dn6_kernel(
     int R, int n_hot, const int64_t* __restrict__ down_w, const int64_t* __restrict__ down_s,
     const _Float16* __restrict__ act, const uint8_t* __restrict__ sh_dw, float* __restrict__ y32,
     int* __restrict__ nparts_out)
 {
-    __shared__ const uint8_t* tab[2][HMOE_MAXE];
-    __shared__ const uint8_t* ptr[2][MAXSLOT];
-    __shared__ f32x4 red[2][DW][64];
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, tok = l & 15, ks = l >> 4, row = l & 15;
+    // one LDS block laid out by hand: the reduction buffer and the tables at the bottom, so that every access in the
+    // item loop is one base register plus an immediate offset (below 64 KB), then the shared act
+    constexpr int O_RED = 0, O_TAB = O_RED + 2 * DW * 64 * 16, O_PTR = O_TAB + 2 * HMOE_MAXE * 8;
+    constexpr int O_XSH = O_PTR + 2 * MAXSLOT * 8, N_SMEM = O_XSH + (SH ? MAXR * XSH_LD * 2 : 0);
+    static_assert(O_XSH <= 65536, "the item loop's LDS must sit below 64 KB");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[N_SMEM];
+    auto& tab = *reinterpret_cast<const uint8_t* (*)[2][HMOE_MAXE]>(smem + O_TAB);
+    auto& ptr = *reinterpret_cast<const uint8_t* (*)[2][MAXSLOT]>(smem + O_PTR);
+    auto& red = *reinterpret_cast<f32x4 (*)[2][DW][64]>(smem + O_RED);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
     const int sw = w >> 2, kq = w & 3;                          // routed items: slot of the quad, k quarter of I
-    const bool live = tok < R;
     const int G = gridDim.x, b = blockIdx.x;
     const int part0 = SH ? 1 : 0, nsh = SH ? NB_H : 0;
     const int s_mine = SH ? (b + G < NB_H ? 2 : 1) : 0;       // (G <= NB_H: every workgroup has one)
@@ -373,20 +385,25 @@ __global__ void __launch_bounds__(DW * 64) dn6_kernel(
     const int64_t t1 = ldg<int64_t>(n_hot > 0 ? down_s + te : (const int64_t*) rec);
     const int rm = ldg<int>(rec), re = ldg<int>(rec + REC_E + min((int) threadIdx.x, MAXSLOT - 1));
     __builtin_amdgcn_sched_barrier(0);                          // keep the routing loads ahead of the item loads
-    // shared items: wave w owns k group w of I (4 k steps of F16T) with the shared act of its k group as the A operand,
-    // formed from the fp32 sums (loaded first, so forming it does not wait for the tiles); the second item is the
-    // first one again when there is none (an L2 hit)
-    f16x8 xs[4];
+    // shared items: wave w owns k group w of I (4 k steps of F16T) with the shared act of its k group as the A operand.
+    // The act f16(silu(g) u) of the R live rows is formed once per workgroup into xsh, 4 elements per thread in each
+    // of NJ steps, from the fp32 sums loaded first, so forming it does not wait for the tiles; the waves read their
+    // fragments after the table barrier. Past R * I / 4 the loads repeat the last float4 (one cache line per wave)
+    // and nothing is stored. The second shared item is the first one again when there is none (an L2 hit).
+    auto& xsh = *reinterpret_cast<_Float16 (*)[MAXR][XSH_LD]>(smem + O_XSH);     // (SH only)
     u32x4 S0[4], S1[4];
     if (SH)
     {
-        const float* shp = (const float*) (act + (size_t) SHP_SLOT * MAXR * I) + (size_t) (live ? tok : 0) * I + 128 * w + 8 * ks;
-        u32x4 gv[8], uv[8];
+        const float* shp = (const float*) (act + (size_t) SHP_SLOT * MAXR * I);
+        const int nq4 = R * (I / 4);
+        u32x4 gv[NJ], uv[NJ];
         #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int j = 0; j < NJ; ++j)
         {
-            gv[2 * t] = ld16(shp + 32 * t); gv[2 * t + 1] = ld16(shp + 32 * t + 4);
-            uv[2 * t] = ld16(shp + MAXR * I + 32 * t); uv[2 * t + 1] = ld16(shp + MAXR * I + 32 * t + 4);
+            const int q = min((int) threadIdx.x + DW * 64 * j, nq4 - 1);
+            const size_t o = (size_t) (q >> 9) * I + (q & 511) * 4;
+            gv[j] = ld16(shp + o);
+            uv[j] = ld16(shp + MAXR * I + o);
         }
         const uint8_t* w0 = sh_dw + ((size_t) (b * KS_I + 4 * w) * 64 + l) * 16;
         const uint8_t* w1 = sh_dw + ((size_t) ((s_mine == 2 ? b + G : b) * KS_I + 4 * w) * 64 + l) * 16;
@@ -396,21 +413,14 @@ __global__ void __launch_bounds__(DW * 64) dn6_kernel(
         for (int k = 0; k < 4; ++k) S1[k] = ldw16(w1 + k * 1024);
         __builtin_amdgcn_sched_barrier(0);
         #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int j = 0; j < NJ; ++j)
         {
-            f16x8 v;
+            const int q = (int) threadIdx.x + DW * 64 * j;
+            f16x4 v;
             #pragma unroll
-            for (int e = 0; e < 8; ++e)
-            {
-                const float g = __uint_as_float(gv[2 * t + (e >> 2)][e & 3]), u = __uint_as_float(uv[2 * t + (e >> 2)][e & 3]);
-                v[e] = (_Float16) (silu(g) * u);
-            }
-            xs[t] = live ? v : (f16x8) {};
+            for (int e = 0; e < 4; ++e) v[e] = (_Float16) (silu(__uint_as_float(gv[j][e])) * __uint_as_float(uv[j][e]));
+            if (q < nq4) *(f16x4*) &xsh[q >> 9][(q & 511) * 4] = v;
         }
-        // formed here, before the barriers below: sunk to its use, the fp32 sums would stay live next to the shared
-        // tiles and push those into scratch
-        #pragma unroll
-        for (int t = 0; t < 4; ++t) asm volatile("" :: "v"(__builtin_bit_cast(u32x4, xs[t])));
     }
     // every thread stores (threads past n_hot repeat entry n_hot - 1 with its own value): a store under a branch
     // would pull the table loads into it, behind the item loads
@@ -428,10 +438,15 @@ __global__ void __launch_bounds__(DW * 64) dn6_kernel(
     __syncthreads();
     int r0, nr;
     {
-        const long long rt_n = (long long) nq * NB_H, T = nsh + rt_n;
+        // the routed items are split by cost, not by count: a workgroup whose range crosses into the next slot quad
+        // reloads that quad's act (4 slots x R rows x I), so every quad is preceded by xc virtual items; a range that
+        // starts among them starts at the quad's first item, one that ends among them ends at the quad's end
+        const long long xc = DN_XCOST(R), span = NB_H + xc, V = (long long) nq * span, T = nsh + V;
         auto start = [&](int bb) {                              // routed items before workgroup bb
             const long long sh_before = (long long) (nsh / G) * bb + min(bb, nsh % G);
-            return (int) max(0ll, min(rt_n, T * bb / G - sh_before));
+            const long long v = max(0ll, min(V, T * bb / G - sh_before));
+            const long long q = v / span;
+            return (int) (q * NB_H + max(v - q * span - xc, 0ll));
         };
         r0 = start(b);
         nr = max(0, start(b + 1) - r0);
@@ -444,8 +459,9 @@ __global__ void __launch_bounds__(DW * 64) dn6_kernel(
         const int it = r0 + min(i, max(nr - 1, 0)), qd = it / NB_H, nb = it - qd * NB_H, j = 4 * qd + sw;
         const bool ok = j < m;
         const int jj = max(min(j, m - 1), 0), nbb = ok ? nb : 0;
-        const size_t toff = ((size_t) (nbb * KG_I + 4 * kq) * 64 + l) * 16;
-        const size_t soff = ((size_t) (nbb * 16 + row) * KG_I + 4 * kq) * 2;
+        // (offsets in 32-bit arithmetic, zero-extended per item: a 64-bit lane term would stay live across the loop)
+        const size_t toff = (uint32_t) (((nbb * KG_I + 4 * kq) * 64 + l) * 16);
+        const size_t soff = (uint32_t) (((nbb * 16 + (l & 15)) * KG_I + 4 * kq) * 2);
         const int kst = (ok && i < nr) ? 1024 : 0;
         #pragma unroll
         for (int k = 0; k < 4; ++k) S.d[k] = ldw16(ptr[0][jj] + toff + k * kst);
@@ -492,6 +508,22 @@ __global__ void __launch_bounds__(DW * 64) dn6_kernel(
     };
     if (SH)
     {
+        // the wave's A fragments of the shared act (rows past R are zero), addressed from an opaque copy of the thread
+        // index so that nothing derived here is shared with (and kept live into) the item loop
+        f16x8 xs[4];
+        {
+            int tid;
+            asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int) threadIdx.x));
+            const int tk = tid & 15;
+            const bool lv = tk < R;
+            const _Float16* xr = &xsh[lv ? tk : 0][128 * (tid >> 6) + 8 * ((tid >> 4) & 3)];
+            #pragma unroll
+            for (int t = 0; t < 4; ++t)
+            {
+                const f16x8 v = *(const f16x8*) (xr + 32 * t);
+                xs[t] = lv ? v : (f16x8) {};
+            }
+        }
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         #pragma unroll
         for (int t = 0; t < 4; ++t) acc = mfma16(xs[t], as_f16x8(S0[t]), acc);
@@ -613,10 +645,14 @@ static int run_decode(const DecodeArgs& a, int phases, hipStream_t st)
     {
         const int gd = min(max(G, DN_GMIN), DN_GMAX);
         if (sh)
-            dn6_kernel<true><<<gd, DW * 64, 0, st>>>(R, a.n_hot, a.down_w, a.down_s, a.act, (const uint8_t*) a.sh_dw,
-                                                     a.y32, a.ctr);
+        {
+            // NJ: float4 steps per thread to form the shared act of R rows (R * 512 float4 over 1024 threads)
+            auto k = R <= 2 ? dn6_kernel<true, 1> : R <= 4 ? dn6_kernel<true, 2> : R <= 8 ? dn6_kernel<true, 4>
+                                                                                        : dn6_kernel<true, 8>;
+            k<<<gd, DW * 64, 0, st>>>(R, a.n_hot, a.down_w, a.down_s, a.act, (const uint8_t*) a.sh_dw, a.y32, a.ctr);
+        }
         else
-            dn6_kernel<false><<<gd, DW * 64, 0, st>>>(R, a.n_hot, a.down_w, a.down_s, a.act, nullptr, a.y32, a.ctr);
+            dn6_kernel<false, 1><<<gd, DW * 64, 0, st>>>(R, a.n_hot, a.down_w, a.down_s, a.act, nullptr, a.y32, a.ctr);
     }
     if (phases & 8) dec_d_kernel<<<(R * H / 4 + 255) / 256, 256, 0, st>>>(a.y32, a.ctr, R, a.y, a.out);
     return HMOE_LAUNCHED("moe4");

@@ -9,6 +9,7 @@
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -105,7 +106,9 @@ __device__ __forceinline__ u32x4 ldw16(const void* p) { return __builtin_nontemp
 __device__ __forceinline__ u32x4 ld16(const void* p) { return ldg<u32x4>(p); }
 __device__ __forceinline__ u32x2 ld8(const void* p) { return ldg<u32x2>(p); }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+// silu(g) = g / (1 + e^-g) with the hardware reciprocal (1 ulp) in place of a correctly rounded division: the result
+// is rounded to f16 next, and the division's refinement sequence is ten VALU instructions per element
+__device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
 // the inputs of one row's selection held by a lane: logits and bias of experts lane + 64 i (i < 4)
 struct RowIn { float lg[4], b[4]; };
