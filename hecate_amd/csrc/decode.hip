@@ -120,11 +120,12 @@ __device__ __forceinline__ void group_i4(const f16x8* xa, u32x4 wq, float s, f32
     for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(s, p[i], acc[i]);
 }
 
-// ---- router logits: two experts per 512-thread workgroup (pair_logits) ----
-__global__ void __launch_bounds__(NT) router_kernel(const uint16_t* __restrict__ x, int R, const float* __restrict__ wt,
-                                                    int E, float* __restrict__ logits)
+// ---- router logits: one expert per 256-thread workgroup (pair_logits), so the 6.3 MB of weight rows spread over
+// every CU (two per workgroup halve the x staging but leave half the CUs idle) ----
+__global__ void __launch_bounds__(256) router_kernel(const uint16_t* __restrict__ x, int R, const float* __restrict__ wt,
+                                                     int E, float* __restrict__ logits)
 {
-    pair_logits<false>(x, NormIn{}, wt, 2 * blockIdx.x, E, R, logits);
+    pair_logits<false, 1>(x, NormIn{}, wt, blockIdx.x, E, R, logits);
 }
 
 // ---- RMSNorm of the residual + router logits (nr4_kernel.cuh:122-381), the same workgroups ----
@@ -627,7 +628,7 @@ static int run_decode(const DecodeArgs& a, int phases, hipStream_t st)
     const bool sh = a.sh_gw != nullptr;
     const int G = a.blocks ? a.blocks : default_grid(1);
     if ((phases & 1) && a.logits)
-        router_kernel<<<(a.E + 1) / 2, NT, 0, st>>>((const uint16_t*) a.x, R, a.wt, a.E, a.logits);
+        router_kernel<<<a.E, 256, 0, st>>>((const uint16_t*) a.x, R, a.wt, a.E, a.logits);
     if (phases & 2)
     {
         int64_t* so = a.logits ? a.sel_out : (int64_t*) a.sel_in;

@@ -283,7 +283,8 @@ struct NormIn
     _Float16* xh;
 };
 
-// logits of experts e0 and e0 + 1 (those < E) for R <= MAXR rows over K = H, by a 512-thread workgroup, in the order of
+// logits of experts e0 .. e0 + EPW - 1 (those < E) for R <= MAXR rows over K = H, by a workgroup of EPW x 256 threads
+// (EPW 1 or 2: more experts per workgroup share its x staging, fewer spread the weight rows over more CUs), in the order of
 // expert_logits with every global load coalesced: the two weight rows, then each group of 4 rows of x, are staged in
 // LDS (consecutive threads on consecutive 16-byte pieces) in a chunk-major layout padded to 144 B (weights) and 80 B
 // (x) per chunk, so a thread's 16-byte reads of its own chunk are free of bank conflicts (8 lanes cover the 32 banks);
@@ -294,21 +295,24 @@ struct NormIn
 constexpr int LCH = H / RCHUNK;             // 192 chunks
 constexpr int WST = RCHUNK + 4;             // weight chunk stride, floats
 constexpr int XST = RCHUNK / 2 + 4;         // x chunk stride, u32 words (two bf16 each)
-template <bool NORM>
+template <bool NORM, int EPW = 2>
 __device__ inline void pair_logits(const uint16_t* __restrict__ x, const NormIn& nin, const float* __restrict__ wt,
                                    int e0, int E, int R, float* __restrict__ logits)
 {
-    __shared__ __attribute__((aligned(16))) float ws[2][LCH * WST];
+    static_assert(EPW == 1 || EPW == 2, "one or two experts per workgroup");
+    static_assert(!NORM || EPW == 2, "the RMSNorm input path splits rows over two halves of 256 threads");
+    constexpr int NTH = 256 * EPW, XP = 3072 / NTH;             // threads; x pieces per thread and group of 4 rows
+    __shared__ __attribute__((aligned(16))) float ws[EPW][LCH * WST];
     __shared__ __attribute__((aligned(16))) uint32_t xs[4][LCH * XST];
-    __shared__ __attribute__((aligned(16))) float sums[2][LCH][MAXR + 1];
-    __shared__ float segs[2][MAXR][RSEG];
+    __shared__ __attribute__((aligned(16))) float sums[EPW][LCH][MAXR + 1];
+    __shared__ float segs[EPW][MAXR][RSEG];
     __shared__ float rmfs[MAXR];
     const int t = threadIdx.x, half = t >> 8, c = t & 255;
-    // the two weight rows: 2 x 1536 pieces of 4 floats, 6 per thread (a row past E re-reads row E - 1)
+    // the weight rows: EPW x 1536 pieces of 4 floats, 6 per thread (a row past E re-reads row E - 1)
     #pragma unroll
     for (int i = 0; i < 6; ++i)
     {
-        const int p = t + 512 * i, h = p / 1536, q = p - h * 1536;
+        const int p = t + NTH * i, h = p / 1536, q = p - h * 1536;
         const f32x4 v = *(const f32x4*) (wt + (size_t) min(e0 + h, E - 1) * H + 4 * q);
         *(f32x4*) &ws[h][(q >> 3) * WST + 4 * (q & 7)] = v;
     }
@@ -337,31 +341,31 @@ __device__ inline void pair_logits(const uint16_t* __restrict__ x, const NormIn&
         if (t < R) rmfs[t] = 1.0f / __builtin_sqrtf(part[t][0] / (float) H + nin.eps);
         __syncthreads();                                        // (sums is written again by the chains below)
     }
-    // rows r0 .. r0 + 3 of x: 4 x 768 pieces of 8 bf16, 6 per thread (rows past R re-read row R - 1); the next
+    // rows r0 .. r0 + 3 of x: 4 x 768 pieces of 8 bf16, XP per thread (rows past R re-read row R - 1); the next
     // group's loads are in flight while the current group computes (NORM: formed at the start of each group, and
     // piece q of a live row also stored to xn by workgroup q * G / 768)
-    u32x4 nx[6];
+    u32x4 nx[XP];
     auto load_x = [&](int r0) {
         #pragma unroll
-        for (int i = 0; i < 6; ++i)
+        for (int i = 0; i < XP; ++i)
         {
-            const int p = t + 512 * i, j = p / 768, q = p - j * 768;
+            const int p = t + NTH * i, j = p / 768, q = p - j * 768;
             nx[i] = *(const u32x4*) (x + (size_t) min(r0 + j, R - 1) * H + 8 * q);
         }
     };
     auto store_x = [&]() {
         #pragma unroll
-        for (int i = 0; i < 6; ++i)
+        for (int i = 0; i < XP; ++i)
         {
-            const int p = t + 512 * i, j = p / 768, q = p - j * 768;
+            const int p = t + NTH * i, j = p / 768, q = p - j * 768;
             *(u32x4*) &xs[j][(q >> 2) * XST + 4 * (q & 3)] = nx[i];
         }
     };
     auto form_x = [&](int r0) {
         #pragma unroll
-        for (int i = 0; i < 6; ++i)
+        for (int i = 0; i < XP; ++i)
         {
-            const int p = t + 512 * i, j = p / 768, q = p - j * 768, row = min(r0 + j, R - 1);
+            const int p = t + NTH * i, j = p / 768, q = p - j * 768, row = min(r0 + j, R - 1);
             const float* hp = nin.h + (size_t) row * H + 8 * q;
             const f32x4 h0 = *(const f32x4*) hp, h1 = *(const f32x4*) (hp + 4);
             const f32x4 w0 = *(const f32x4*) (nin.w + 8 * q), w1 = *(const f32x4*) (nin.w + 8 * q + 4);
@@ -438,7 +442,7 @@ __device__ inline void pair_logits(const uint16_t* __restrict__ x, const NormIn&
     }
     // the fold: segment sums (chunks in order) by one thread per (expert, row, segment), then the segments in order
     constexpr int cps = LCH / RSEG;
-    if (t < 2 * R * RSEG)
+    if (t < EPW * R * RSEG)
     {
         const int h = t / (R * RSEG), rem = t - h * R * RSEG, r = rem / RSEG, sg = rem - r * RSEG;
         float seg = 0.f;
