@@ -172,7 +172,13 @@ def tiered_workload(torch, synth, steps, warmup, dev, threads=8):
     from hecate_amd.cpu_tier import CpuTier, decode_split, host_experts
     lay = synth.make_layer(0, dev, resident=synth.popularity_order()[:176], shared=False)
     cpu = CpuTier(threads=threads)
-    out = {"cpu_threads": threads}
+    try:
+        with open("/proc/cpuinfo") as f:
+            flags = next((ln for ln in f if ln.startswith("flags")), "").split()
+    except OSError:
+        flags = []
+    vnni = "avx512_vnni" in flags and "avx512bw" in flags and os.environ.get("HMOE_CPU_ISA") != "avx2"
+    out = {"cpu_threads": threads, "cpu_dot": "avx512-vnni" if vnni else "avx2"}
     try:
         cpu.add_layer(0, 176, host_experts(0, lay.perm[176:], dev))
         for R in (1, 4, 8):

@@ -17,6 +17,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <immintrin.h>
 #include <mutex>
@@ -143,6 +144,79 @@ static void gemv(const Mat& m, int K, const int8_t* xq, const float* xs, int nr,
     }
 }
 
+// ---- the same GEMV with AVX-512 VNNI (used when the host has it; same integer lane sums, same bits) ----
+// The input rows are first laid out per group of 128 as VG bytes: xa (k 0..15 of blocks 0..3, 16 bytes each), xb (k
+// 16..31 of each block), then 16 int32 init[4 b + i] = -8 * (the sum of x over lane i of block b). vpdpbusd of the
+// unsigned codes (z + 8) against xa and xb, started from init, leaves in dword 4 b + i exactly block_dot's lane i of
+// block b: sum z x = sum (z + 8) x - 8 sum x, all in int32.
+constexpr int VG = 192;
+
+#define HMOE_VNNI __attribute__((target("avx512f,avx512bw,avx512vnni")))
+
+HMOE_VNNI static void to_vnni(const int8_t* xq, int K, uint8_t* out)
+{
+    const __m512i ones = _mm512_set1_epi8(1);
+    for (int g = 0; g < K / 128; ++g)
+    {
+        const __m512i b01 = _mm512_loadu_si512(xq + (size_t) g * 128);        // [b0 lo, b0 hi, b1 lo, b1 hi]
+        const __m512i b23 = _mm512_loadu_si512(xq + (size_t) g * 128 + 64);
+        const __m512i xa = _mm512_shuffle_i64x2(b01, b23, 0x88), xb = _mm512_shuffle_i64x2(b01, b23, 0xdd);
+        const __m512i sx = _mm512_dpbusd_epi32(_mm512_dpbusd_epi32(_mm512_setzero_si512(), ones, xa), ones, xb);
+        uint8_t* o = out + (size_t) g * VG;
+        _mm512_storeu_si512(o, xa);
+        _mm512_storeu_si512(o + 64, xb);
+        _mm512_storeu_si512(o + 128, _mm512_sub_epi32(_mm512_setzero_si512(), _mm512_slli_epi32(sx, 3)));
+    }
+}
+
+HMOE_VNNI static void gemv_vnni(const Mat& m, int K, const int8_t* xq, const float* xs, int nr, int n0, int n1, float* y,
+                                int ys)
+{
+    const int NG = K / 128;
+    static thread_local std::vector<uint8_t> xv((size_t) CMAXR * (H / 128) * VG);
+    for (int r = 0; r < nr; ++r) to_vnni(xq + (size_t) r * K, K, xv.data() + (size_t) r * NG * VG);
+    const __m512i lo4 = _mm512_set1_epi8(0x0f);
+    for (int n = n0; n < n1; ++n)
+    {
+        const uint8_t* qr = m.q + (size_t) n * (K / 2);
+        const uint16_t* sr = m.s + (size_t) n * NG;
+        float yr[CMAXR];
+        for (int r = 0; r < nr; ++r) yr[r] = 0.0f;
+        for (int g = 0; g < NG; ++g)
+        {
+            // the group's 4 blocks, one per 128-bit lane: k 0..15 and k 16..31 of each as unsigned codes
+            const __m512i raw = _mm512_loadu_si512(qr + (size_t) g * 64);
+            const __m512i lo = _mm512_and_si512(raw, lo4), hi = _mm512_and_si512(_mm512_srli_epi16(raw, 4), lo4);
+            const __m512i za = _mm512_unpacklo_epi8(lo, hi), zb = _mm512_unpackhi_epi8(lo, hi);
+            const float sc = bf2f(sr[g]);
+            for (int r = 0; r < nr; ++r)
+            {
+                const uint8_t* xg = xv.data() + ((size_t) r * NG + g) * VG;
+                __m512i d = _mm512_dpbusd_epi32(_mm512_loadu_si512(xg + 128), za, _mm512_loadu_si512(xg));
+                d = _mm512_dpbusd_epi32(d, zb, _mm512_loadu_si512(xg + 64));
+                const __m512 f = _mm512_cvtepi32_ps(d);
+                const float* xsr = xs + (size_t) r * (K / 32) + 4 * g;
+                __m128 acc = _mm_fmadd_ps(_mm512_castps512_ps128(f), _mm_set1_ps(xsr[0]), _mm_setzero_ps());
+                acc = _mm_fmadd_ps(_mm512_extractf32x4_ps(f, 1), _mm_set1_ps(xsr[1]), acc);
+                acc = _mm_fmadd_ps(_mm512_extractf32x4_ps(f, 2), _mm_set1_ps(xsr[2]), acc);
+                acc = _mm_fmadd_ps(_mm512_extractf32x4_ps(f, 3), _mm_set1_ps(xsr[3]), acc);
+                alignas(16) float a[4];
+                _mm_store_ps(a, acc);
+                yr[r] = std::fma(sc, (a[0] + a[1]) + (a[2] + a[3]), yr[r]);
+            }
+        }
+        for (int r = 0; r < nr; ++r) y[(size_t) r * ys + n] = yr[r];
+    }
+}
+
+static bool g_vnni = false;                         // the host has AVX-512 VNNI (decided at pool start)
+
+static void gemv_any(const Mat& m, int K, const int8_t* xq, const float* xs, int nr, int n0, int n1, float* y, int ys)
+{
+    if (g_vnni) gemv_vnni(m, K, xq, xs, nr, n0, n1, y, ys);
+    else gemv(m, K, xq, xs, nr, n0, n1, y, ys);
+}
+
 static void range(int total, int t, int T, int& a, int& b)
 {
     a = (int) ((long long) total * t / T);
@@ -211,8 +285,8 @@ static void run_job(Pool& p, int t)
         }
         int a, b;
         range(I, t, T, a, b);
-        gemv(ex.gate, H, xqp.data(), xsp.data(), nr, a, b, w.gy.data(), I);
-        gemv(ex.up, H, xqp.data(), xsp.data(), nr, a, b, w.uy.data(), I);
+        gemv_any(ex.gate, H, xqp.data(), xsp.data(), nr, a, b, w.gy.data(), I);
+        gemv_any(ex.up, H, xqp.data(), xsp.data(), nr, a, b, w.uy.data(), I);
         barrier(p);
         range(nr * I / 32, t, T, a, b);
         for (int gi = a; gi < b; ++gi)
@@ -240,7 +314,7 @@ static void run_job(Pool& p, int t)
         {
             const Expert& ex = ly->ex[w.pick[q]];
             const int nr = w.nrows[q];
-            gemv(ex.down, I, w.aq.data() + (size_t) q * CMAXR * I, w.as.data() + (size_t) q * CMAXR * I / 32, nr, a, b,
+            gemv_any(ex.down, I, w.aq.data() + (size_t) q * CMAXR * I, w.as.data() + (size_t) q * CMAXR * I / 32, nr, a, b,
                  y1.data(), H);
             for (int j = 0; j < nr; ++j)
             {
@@ -299,6 +373,11 @@ extern "C" int hmoe_cpu_start(hmoe_cpu_mailbox* mb, int threads, int first_core)
     std::lock_guard<std::mutex> lk(g_mu);
     if (g_pool) return hmoe::set_error(HMOE_ERR_ARG, "cpu_start: the pool is running");
     if (!mb || threads < 1 || threads > 256) return hmoe::set_error(HMOE_ERR_ARG, "cpu_start: mailbox / threads");
+    // the dot kernel: AVX-512 VNNI where the host has it, unless HMOE_CPU_ISA=avx2 asks for the AVX2 one (both give
+    // the same bits)
+    const char* isa = std::getenv("HMOE_CPU_ISA");
+    g_vnni = __builtin_cpu_supports("avx512vnni") && __builtin_cpu_supports("avx512bw") &&
+             !(isa && std::strcmp(isa, "avx2") == 0);
     Pool* p = new Pool();
     p->mb = mb;
     p->nthr = threads;

@@ -1,7 +1,7 @@
 """The host-CPU expert tier (hecate_amd/csrc/cputier.cpp) driven from the host through a plain-memory mailbox, as
 tools/dev/test_grace_picks.py drives cpuband's flags: bit-exact against the oracle's q8_0 mode (cpuband.cpp's
 arithmetic), a many-pick job equal to the sum of its one-pick jobs (test_grace_picks.py:95-152), the same bits for
-any thread count, and the error words of bad jobs. No GPU."""
+any thread count and for either dot kernel (AVX2, AVX-512 VNNI), and the error words of bad jobs. No GPU."""
 import numpy as np
 import pytest
 
@@ -116,3 +116,24 @@ def test_cpu_tier_bad_jobs(cold):
         assert err == 1
     finally:
         t.close()
+
+
+def test_cpu_tier_dot_kernels_agree(cold, monkeypatch):
+    """the AVX2 dot and the AVX-512 VNNI dot (taken when the host has it) give the same bits: the same integer lane
+    sums reach the same float order (HMOE_CPU_ISA=avx2 forces the first at pool start)"""
+    R = 6
+    x = x_rows(41, R)
+    sel, rw = picks(R, 13)
+    outs = []
+    for isa in ("avx2", None):
+        if isa:
+            monkeypatch.setenv("HMOE_CPU_ISA", isa)
+        else:
+            monkeypatch.delenv("HMOE_CPU_ISA", raising=False)
+        t = start(cold, 3)
+        try:
+            t.post(x, sel, rw, 0)
+            outs.append(t.wait()[0])
+        finally:
+            t.close()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
