@@ -134,27 +134,11 @@ __device__ __forceinline__ void load_bias_global(const float* __restrict__ bias,
     }
 }
 
-// (hi, lo) <- the larger of the 64-bit keys (hi, lo) and (h2, l2)
-__device__ __forceinline__ void max_key(uint32_t& hi, uint32_t& lo, uint32_t h2, uint32_t l2)
-{
-    const bool gt = h2 > hi || (h2 == hi && l2 > lo);
-    hi = gt ? h2 : hi;
-    lo = gt ? l2 : lo;
-}
-// one step of a 16-lane row reduction: combine with the key of the lane DPP control CTRL names (the quad permutations
-// and row rotations used here keep every source lane inside the row)
-template <int CTRL>
-__device__ __forceinline__ void max_key_dpp(uint32_t& hi, uint32_t& lo)
-{
-    const uint32_t h2 = (uint32_t) __builtin_amdgcn_mov_dpp((int) hi, CTRL, 0xf, 0xf, false);
-    const uint32_t l2 = (uint32_t) __builtin_amdgcn_mov_dpp((int) lo, CTRL, 0xf, 0xf, false);
-    max_key(hi, lo, h2, l2);
-}
-
-// top-k of one row by a wave (all 64 lanes active): keys of experts lane + 64 i; each round takes the largest
-// (key, -index) pair, so ties go to the lowest index (exl3_router.py:106-121); the sum runs over the selected unbiased
-// activations in order. A round reduces each 16-lane row with DPP (lane pairs, quad pairs, rotations by 4 and 8) and
-// the four row maxima in scalar registers, so the winner is wave-uniform.
+// top-k of one row by a wave (all 64 lanes active): keys of experts lane + 64 i; the selection is the one of taking
+// the largest (key, -index) pair topk times, so ties go to the lowest index and sel is in descending key order
+// (exl3_router.py:106-121); the sum runs over the selected unbiased activations in that order. It is found without
+// those rounds: the topk-th largest key by a bitwise threshold search on wave ballots, then each pick's position from
+// ballot counts; every step is wave-uniform.
 __device__ inline void select_from(const RowIn& in, int E, int topk, float scale, int64_t* __restrict__ sel,
                                    uint16_t* __restrict__ rw)
 {
@@ -171,32 +155,62 @@ __device__ inline void select_from(const RowIn& in, int E, int topk, float scale
         }
         else { a[i] = 0.f; key[i] = 0u; }
     }
-    float sum = 0.f, wsel = 0.f; int isel = 0;
-    for (int k = 0; k < topk; ++k)
+    // T: the topk-th largest key (the largest T with at least topk keys >= T), found one bit at a time with wave
+    // ballots (a chain of 32 short steps, where taking the maximum topk times is a chain of cross-lane reductions)
+    uint32_t T = 0u;
+    for (int bit = 31; bit >= 0; --bit)
     {
-        uint32_t hi = key[0], lo = 0xffffu - lane;
+        const uint32_t c = T | (1u << bit);
+        int n = 0;
         #pragma unroll
-        for (int i = 1; i < 4; ++i) max_key(hi, lo, key[i], 0xffffu - (lane + 64 * i));
-        max_key_dpp<0xb1>(hi, lo);                               // quad_perm [1, 0, 3, 2]
-        max_key_dpp<0x4e>(hi, lo);                               // quad_perm [2, 3, 0, 1]
-        max_key_dpp<0x124>(hi, lo);                              // row_ror 4
-        max_key_dpp<0x128>(hi, lo);                              // row_ror 8
-        uint32_t bh = __builtin_amdgcn_readlane(hi, 0), bl = __builtin_amdgcn_readlane(lo, 0);
-        #pragma unroll
-        for (int r = 1; r < 4; ++r)
-            max_key(bh, bl, __builtin_amdgcn_readlane(hi, 16 * r), __builtin_amdgcn_readlane(lo, 16 * r));
-        const int e = 0xffff - (int) (bl & 0xffffu), wl = e & 63, wi = e >> 6;
-        #pragma unroll
-        for (int i = 0; i < 4; ++i) key[i] = (lane == wl && i == wi) ? 0u : key[i];
-        const float aw = wi == 0 ? a[0] : (wi == 1 ? a[1] : (wi == 2 ? a[2] : a[3]));
-        const float av = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(aw), wl));
-        sum = sum + av;
-        if (lane == k) { wsel = av; isel = e; }
+        for (int i = 0; i < 4; ++i) n += __popcll(__ballot(key[i] >= c));
+        if (n >= topk) T = c;
     }
+    // the picks: every key above T, then keys equal to T by ascending expert id (id lane + 64 i: i-major order)
+    uint64_t pick[4];
+    int need = topk;
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) { pick[i] = __ballot(key[i] > T); need -= __popcll(pick[i]); }
+    #pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        uint64_t eq = __ballot(key[i] == T);
+        while (need > 0 && eq) { const uint64_t low = eq & (~eq + 1ull); pick[i] |= low; eq ^= low; --need; }
+    }
+    // each pick's place in the selection order (key descending, then id ascending): the number of picks before it;
+    // lane r of es / as receives the r-th pick's id and sigmoid
+    int es = 0;
+    float as = 0.f;
+    #pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        uint64_t mk = pick[i];
+        while (mk)
+        {
+            const int l = __builtin_ctzll(mk);
+            mk &= mk - 1ull;
+            const uint32_t kx = (uint32_t) __builtin_amdgcn_readlane((int) key[i], l);
+            const int ex = l + 64 * i;
+            int r = 0;
+            #pragma unroll
+            for (int j = 0; j < 4; ++j)
+            {
+                const int ej = lane + 64 * j;
+                const bool before = ((pick[j] >> lane) & 1ull) && (key[j] > kx || (key[j] == kx && ej < ex));
+                r += __popcll(__ballot(before));
+            }
+            const int ax = __builtin_amdgcn_readlane(__float_as_int(i == 0 ? a[0] : i == 1 ? a[1] : i == 2 ? a[2] : a[3]), l);
+            es = lane == r ? ex : es;
+            as = lane == r ? __int_as_float(ax) : as;
+        }
+    }
+    // the unbiased sigmoids summed in selection order, from 0
+    float sum = 0.f;
+    for (int k = 0; k < topk; ++k) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(as), k));
     if (lane < topk)
     {
-        sel[lane] = isel;
-        rw[lane] = hmoe_f2h((wsel * scale) / (sum + 1e-20f));
+        sel[lane] = es;
+        rw[lane] = hmoe_f2h((as * scale) / (sum + 1e-20f));
     }
 }
 
