@@ -318,23 +318,36 @@ __global__ void __launch_bounds__(256) to_f16_kernel(const uint16_t* __restrict_
     }
 }
 
-// fin, deterministic: out[t] += (sum over k in top-k order of d[inv[t][k]]) (+ the shared expert's row)
+// fin, deterministic: out[t] += (sum over k in top-k order of d[inv[t][k]]) (+ the shared expert's row). Every row's
+// load is unconditional (an absent pick or shared row reads row 0 and is dropped by a select at its add), so all of
+// them are in flight together: under a branch each load was followed by a wait for it.
 __global__ void __launch_bounds__(256) pfin_kernel(const float* __restrict__ d, const int* __restrict__ inv, int topk,
                                                    int sh_off, float* __restrict__ out)
 {
+    constexpr int NR = HMOE_TOPK + 1;
     const int t = blockIdx.x;
-    int pos[HMOE_TOPK];
+    int pos[NR];
+    bool use[NR];
     #pragma unroll
-    for (int k = 0; k < HMOE_TOPK; ++k) pos[k] = k < topk ? inv[(size_t) t * topk + k] : -1;
+    for (int k = 0; k < HMOE_TOPK; ++k)
+    {
+        const int p = k < topk ? inv[(size_t) t * topk + min(k, topk - 1)] : -1;
+        use[k] = p >= 0;
+        pos[k] = max(p, 0);
+    }
+    use[HMOE_TOPK] = sh_off >= 0;
+    pos[HMOE_TOPK] = sh_off >= 0 ? sh_off + t : 0;
     for (int n = threadIdx.x * 4; n < H; n += 256 * 4)
     {
+        f32x4 v[NR];
+        #pragma unroll
+        for (int k = 0; k < NR; ++k) v[k] = *(const f32x4*) (d + (size_t) pos[k] * H + n);
+        f32x4* o = (f32x4*) (out + (size_t) t * H + n);
+        const f32x4 ov = *o;
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
         #pragma unroll
-        for (int k = 0; k < HMOE_TOPK; ++k)
-            if (pos[k] >= 0) s += *(const f32x4*) (d + (size_t) pos[k] * H + n);
-        if (sh_off >= 0) s += *(const f32x4*) (d + (size_t) (sh_off + t) * H + n);
-        f32x4* o = (f32x4*) (out + (size_t) t * H + n);
-        *o = *o + s;
+        for (int k = 0; k < NR; ++k) s = use[k] ? s + v[k] : s;
+        *o = ov + s;
     }
 }
 
