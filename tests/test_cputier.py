@@ -137,3 +137,30 @@ def test_cpu_tier_dot_kernels_agree(cold, monkeypatch):
         finally:
             t.close()
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
+def test_cpu_tier_entry_points_reject_bad_arguments(cold):
+    """the C ABI's checks (before any GPU call): one pool per process, thread counts, layer shapes, the hand-off's
+    row counts and alignment; each failure returns an error code with a message"""
+    import ctypes
+    from hecate_amd import _lib
+    L = _lib.lib()
+    mb = (ctypes.c_uint8 * 200_000)()
+    assert L.hmoe_cpu_stats(None, None) != 0 and b"no pool" in L.hmoe_last_error()
+    assert L.hmoe_cpu_add_layer(0, 0, 0, None, None) != 0
+    assert L.hmoe_cpu_start(ctypes.addressof(mb), 0, -1) != 0 and b"threads" in L.hmoe_last_error()
+    t = start(cold, 2)
+    try:
+        assert L.hmoe_cpu_start(ctypes.addressof(mb), 2, -1) != 0 and b"running" in L.hmoe_last_error()
+        assert L.hmoe_cpu_add_layer(1, 0, 300, None, None) != 0 and b"arguments" in L.hmoe_last_error()
+        buf = np.zeros(1 << 16, np.uint8)
+        p = buf.ctypes.data
+        # rows past the mailbox, a null pointer, a misaligned one: refused before anything is queued
+        assert L.hmoe_cpu_submit(t.addr, p, p, p, 9, 0, None) != 0 and b"rows" in L.hmoe_last_error()
+        assert L.hmoe_cpu_submit(t.addr, None, p, p, 1, 0, None) != 0
+        assert L.hmoe_cpu_submit(t.addr, p + 2, p, p, 1, 0, None) != 0 and b"aligned" in L.hmoe_last_error()
+        assert L.hmoe_cpu_collect(t.addr, p, 0, None) != 0
+        assert L.hmoe_cpu_collect(t.addr, p + 4, 1, None) != 0
+    finally:
+        t.close()
+    assert L.hmoe_cpu_stop() == 0                                # (stopping twice is harmless)
