@@ -4,7 +4,8 @@
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only WORKLOAD]
 
 Headline (`value`): the 16-row decode step (8 requests + 8 draft rows, Zipf(1.1) expert popularity): one MoE layer
-(router + routed int4 experts + shared expert + bf16 output) per step, in tokens/s. Steps cycle over 6 seeded
+(router + routed int4 experts + shared expert + bf16 output) per step, in tokens/s, the steps captured in one hipGraph
+and replayed (eager launches reported beside it). Steps cycle over 6 seeded
 layers and 64 seeded inputs so consecutive steps stream different weights (the working set of a step is far above
 the 256 MB last-level cache, as in a real decode pass through 75+ layers). Extras: decode at 1 and 8 rows, the
 2048-token prefill chunk, the 176-resident partial tier at 1/4/8 rows, the same split with the other 80 experts on the
@@ -54,6 +55,26 @@ def timed(torch, fn, steps, warmup):
     return time.perf_counter() - t0
 
 
+def timed_graph(torch, fn, steps, warmup):
+    """the same steps captured in one hipGraph and replayed, as a decode loop runs its per-row-count step (the
+    reference captures its decode step once per row count, rtx_graph.py:6-8); the timed region is one replay"""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            fn(i)
+    g.replay()                                          # (first replay uploads the graph)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g.replay()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    del g
+    return el
+
+
 def decode_layers(torch, synth, R, n_layers, zipf, dev):
     import numpy as np
     layers = []
@@ -73,7 +94,8 @@ def decode_workload(torch, synth, R, steps, warmup, zipf, dev, n_layers=6, n_x=6
     log(f"[bench] decode R={R}: {n_layers} layers ({sum(l.bank.nbytes for l in layers) / 1e9:.1f} GB) ready in "
         f"{time.perf_counter() - t0:.1f} s")
     L, P = len(layers), len(xs)
-    el = timed(torch, lambda i: layers[i % L].decode(xs[i % P]), steps, warmup)
+    el_eager = timed(torch, lambda i: layers[i % L].decode(xs[i % P]), steps, warmup)
+    el = timed_graph(torch, lambda i: layers[i % L].decode(xs[i % P]), steps, warmup)
     # per-kernel timing of the same steps with HIP events on the launch stream: A (router logits), B (shared + routed
     # gate/up + SwiGLU, gu7_kernel), C (shared + routed down, dn6_kernel), D (ordered reduce + bf16 out)
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
@@ -99,7 +121,8 @@ def decode_workload(torch, synth, R, steps, warmup, zipf, dev, n_layers=6, n_x=6
               float(np.mean(U * DOWN_EXPERT_BYTES + SHARED_DOWN_BYTES + (U + 1) * R * 2048 * 2)),
               0.0]
     names = ["A_router", "B_gate_up", "C_down", "D_reduce_out"]
-    res = {"rows": R, "us_per_step": step_s * 1e6, "us_per_token": step_s * 1e6 / R, "tok_per_s": R / step_s,
+    res = {"rows": R, "us_per_step": step_s * 1e6, "us_per_step_eager": el_eager / steps * 1e6,
+           "us_per_token": step_s * 1e6 / R, "tok_per_s": R / step_s,
            "distinct_experts_mean": float(U.mean()), "bytes_per_step": bytes_step,
            "hbm_gbs": bytes_step / step_s / 1e9, "hbm_frac": bytes_step / step_s / 1e9 / HBM_PEAK_GBS,
            "kernels": {n: {"us": kus[k], "algorithmic_bytes": kbytes[k],
@@ -147,7 +170,8 @@ def partial_workload(torch, synth, steps, warmup, dev, n_layers=4):
             lay = layers[i % n_layers]
             lay.route(xs[i % 32])
             lay.experts_decode(R, part, with_shared=False)
-        el = timed(torch, step, steps, warmup)
+        el_eager = timed(torch, step, steps, warmup)
+        el = timed_graph(torch, step, steps, warmup)
         U = []
         for i in range(steps):
             lay = layers[i % n_layers]
@@ -156,7 +180,8 @@ def partial_workload(torch, synth, steps, warmup, dev, n_layers=4):
         U = np.array(U, np.float64)
         step_s = el / steps
         b = float(np.mean(U * EXPERT_BYTES + ROUTER_BYTES + 2 * R * H * 4 + R * H * 2))
-        out[f"B{R}"] = {"us_per_step": step_s * 1e6, "us_per_token": step_s * 1e6 / R,
+        out[f"B{R}"] = {"us_per_step": step_s * 1e6, "us_per_step_eager": el_eager / steps * 1e6,
+                        "us_per_token": step_s * 1e6 / R,
                         "resident_experts_mean": float(U.mean()), "hbm_gbs": b / step_s / 1e9,
                         "hbm_frac": b / step_s / 1e9 / HBM_PEAK_GBS}
     del layers
