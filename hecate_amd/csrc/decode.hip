@@ -563,24 +563,33 @@ __global__ void __launch_bounds__(DW * 64) dn6_kernel(
 }
 
 // ---- y (+)= sum of the parts in order; or the layer's bf16 output ----
+// one thread per element: the parts are loaded 8 at a time (the first 8 before the part count arrives; a part past the
+// count is read, from inside the buffer, and not added), then added in part order
 __global__ void __launch_bounds__(256) dec_d_kernel(const float* __restrict__ y32, const int* __restrict__ nparts_p,
                                                     int R, float* __restrict__ y, uint16_t* __restrict__ out)
 {
-    const int i = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    static_assert(MAX_PARTS >= 8, "the first batch of parts is read before the part count");
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= R * H) return;
-    const int np = *nparts_p, r = i / H, n = i % H;
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    for (int p = 0; p < np; ++p) s += *(const f32x4*) (y32 + ((size_t) p * MAXR + r) * H + n);
-    if (y)
-    {
-        f32x4* yp = (f32x4*) (y + i);
-        *yp = *yp + s;
-    }
-    if (out)
+    const int r = i / H, n = i - r * H;
+    const float* yp = y32 + (size_t) r * H + n;
+    constexpr size_t PS = (size_t) MAXR * H;                   // one part
+    float v[8];
+    #pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = yp[k * PS];
+    const int np = *nparts_p;
+    float s = 0.f;
+    for (int p = 0;;)
     {
         #pragma unroll
-        for (int k = 0; k < 4; ++k) out[i + k] = hmoe_f2bf(s[k]);
+        for (int k = 0; k < 8; ++k) s = p + k < np ? s + v[k] : s;
+        p += 8;
+        if (p >= np) break;
+        #pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = yp[(size_t) min(p + k, MAX_PARTS - 1) * PS];
     }
+    if (y) y[i] = y[i] + s;
+    if (out) out[i] = hmoe_f2bf(s);
 }
 
 int default_grid(int per_cu)
@@ -655,7 +664,7 @@ static int run_decode(const DecodeArgs& a, int phases, hipStream_t st)
         else
             dn6_kernel<false, 1><<<gd, DW * 64, 0, st>>>(R, a.n_hot, a.down_w, a.down_s, a.act, nullptr, a.y32, a.ctr);
     }
-    if (phases & 8) dec_d_kernel<<<(R * H / 4 + 255) / 256, 256, 0, st>>>(a.y32, a.ctr, R, a.y, a.out);
+    if (phases & 8) dec_d_kernel<<<(R * H + 255) / 256, 256, 0, st>>>(a.y32, a.ctr, R, a.y, a.out);
     return HMOE_LAUNCHED("moe4");
 }
 
