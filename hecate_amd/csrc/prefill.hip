@@ -414,6 +414,8 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
                                   const void* sh_gw, const void* sh_uw, const void* sh_dw, int xf, void* stream)
 {
     (void) eid;
+    // an empty chunk is a no-op, as the reference returns when no pick reaches the tier (moe4p.cu:229)
+    if (T == 0 && npos == 0) return HMOE_OK;
     HMOE_REQUIRE(x && tok && wt && rbt && ar && d && out, "moe4p_forward: null buffer");
     HMOE_REQUIRE(npos >= 0 && nrb >= 0 && npos <= ps && T >= 1 && topk >= 1 && topk <= TOPK,
                  "moe4p_forward: npos %d nrb %d ps %d T %d topk %d", npos, nrb, ps, T, topk);

@@ -227,8 +227,11 @@ class MoELayer:
                       inv=pf.inv[:T * self.topk], meta=pf.meta, topk=self.topk, shared=sh, npos=pf.F, nrb=pf.nrb_max)
 
     def prefill(self, x, with_shared=True):
-        """the prefill layer: bf16 [T, H] out (router, device dispatch plan, grouped GEMMs, per-token combine)"""
+        """the prefill layer: bf16 [T, H] out (router, device dispatch plan, grouped GEMMs, per-token combine); an
+        empty chunk gives an empty output (tier_split.py:377 returns out when no pick reaches the tier)"""
         T = x.shape[0]
+        if T == 0:
+            return torch.empty((0, H), dtype=torch.bfloat16, device=x.device)
         pf = self._prefill_buffers(T)
         sel, rw = pf.sel[:T], pf.rw[:T]
         router.router_fused(x, self.wg, self.bias, pf.logits, self.ctr, sel, rw, self.topk, self.scale, pf.xh[:T])

@@ -37,6 +37,16 @@ def test_error_path_sets_message():
         _lib.call("hmoe_pack_i4", buf.ctypes.data, buf.ctypes.data, 15, 128, buf.ctypes.data, buf.ctypes.data)
 
 
+def test_empty_prefill_chunk_is_a_no_op():
+    """no tokens and no picks: the prefill entry returns before any check of its buffers and before any GPU call
+    (moe4p.cu:229 returns when no pick reaches the tier); tokens without buffers are still refused"""
+    L = _lib.lib()
+    args = [None] * 5 + [0, 0, 0] + [None] * 10 + [0, None, None, 0, 8, None, None, None, 0, None]
+    assert L.hmoe_moe4p_forward(*args) == 0
+    args[21] = 3
+    assert L.hmoe_moe4p_forward(*args) != 0 and b"null" in L.hmoe_last_error()
+
+
 @pytest.mark.parametrize("N,K", [(16, 128), (64, 384), (2048, 6144)])
 def test_pack_unpack_round_trip_and_layout(N, K):
     rng = np.random.default_rng(N)

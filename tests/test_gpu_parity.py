@@ -397,6 +397,27 @@ def test_prefill_parity(dev):
     assert ma <= MAX_ABS and mr <= MEAN_REL
 
 
+def test_prefill_empty_and_no_picks(dev):
+    """the reference's early returns (moe4p.cu:229 when no pick reaches the tier, tier_split.py:377): an empty chunk
+    gives an empty output without an error, and a call with no picks and no shared expert leaves out untouched"""
+    log("prefill T=0 and npos=0")
+    lay = gpu_layer("c2", dev, layer=0, bias_sigma=0.001, max_rows=2048)
+    out = lay.prefill(torch.empty((0, H), dtype=torch.bfloat16, device=dev))
+    assert out.shape == (0, H) and out.dtype == torch.bfloat16
+    T = 5
+    pf = lay._prefill_buffers(T)
+    gq, uq, dq, gs, us, ds = lay.bank.tables()
+    xe = torch.empty((0, H), dtype=torch.float16, device=dev)
+    moe4p.forward(xe, pf.tok, pf.eid, pf.wt, pf.rbt, gq, uq, dq, gs, us, ds, *pf.scr, pf.y[:0], meta=pf.meta, npos=0,
+                  nrb=0)
+    y = torch.randn(T, H, device=dev)
+    y0 = y.clone()
+    moe4p.forward(pf.xh[:T], pf.tok, pf.eid, pf.wt, pf.rbt, gq, uq, dq, gs, us, ds, *pf.scr, y, meta=pf.meta, npos=0,
+                  nrb=0)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y0)
+
+
 @pytest.mark.parametrize("T", [1, 37, 300])
 def test_prefill_ragged(dev, T):
     """prefill chunks that are not a multiple of the 128-row block (the shared expert's last block partial, experts
