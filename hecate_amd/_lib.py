@@ -87,6 +87,17 @@ def ptr(t):
     return t.ctypes.data
 
 
+def on_device(what, x, *ts):
+    """raise unless x is a CUDA tensor and every other tensor given (None skipped) is on x's device: a host pointer
+    handed to a kernel faults the GPU instead of raising"""
+    dev = getattr(x, "device", None)
+    if dev is None or dev.type != "cuda":
+        raise RuntimeError(f"{what}: x must be a device tensor")
+    for t in ts:
+        if t is not None and not isinstance(t, int) and getattr(t, "device", None) != dev:
+            raise RuntimeError(f"{what}: every tensor must be on the device {dev}")
+
+
 def stream_of(device=None):
     import torch
     return torch.cuda.current_stream(device).cuda_stream

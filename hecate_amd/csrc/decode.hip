@@ -31,6 +31,8 @@
 //   reduce   y[r] (+)= sum of the parts in order (moe4.cu:826-827 accumulates into y), or the layer's bf16 output
 #include "hmoe_dev.h"
 
+#include <atomic>
+
 namespace hmoe {
 
 constexpr int NW = 8, NT = NW * 64;        // router workgroup
@@ -592,18 +594,20 @@ __global__ void __launch_bounds__(256) dec_d_kernel(const float* __restrict__ y3
     if (out) out[i] = hmoe_f2bf(s);
 }
 
+// per_cu workgroups per CU of the current device (the CU count cached per device; threads that race to fill an
+// entry store the same value)
 int default_grid(int per_cu)
 {
-    static int cus[64] = {0};
+    static std::atomic<int> cus[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256 * per_cu;
-    if (!cus[dev])
+    int v = cus[dev].load(std::memory_order_relaxed);
+    if (!v)
     {
-        int v = 0;
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-        cus[dev] = v;
+        cus[dev].store(v, std::memory_order_relaxed);
     }
-    return cus[dev] * per_cu;
+    return v * per_cu;
 }
 
 struct DecodeArgs

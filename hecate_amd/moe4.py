@@ -6,7 +6,7 @@ expert as F16T. Work runs on the current torch stream; errors raise RuntimeError
 """
 import torch
 
-from ._lib import call, lib, ptr, stream_of
+from ._lib import call, lib, on_device, ptr, stream_of
 
 H, I, TOPK, MAXR = 6144, 2048, 8, 16
 
@@ -38,6 +38,7 @@ def forward(x, sel, rw, n_hot, gate_w, up_w, down_w, gate_s, up_s, down_s, act, 
             blocks_a, lo, sh_gw=0, sh_uw=0, sh_dw=0, sh_gs=0, sh_us=0, sh_ds=0, xf=0):
     """moe4.cu:828-895: y[R][H] (fp32) += routed experts of the picks in [lo, lo + n_hot) (+ the shared expert)"""
     R = x.shape[0]
+    on_device("moe4", x, sel, rw, gate_w, up_w, down_w, gate_s, up_s, down_s, act, gu32, ctr_a, y32, ctr_b, y)
     _req(1 <= R <= MAXR and x.shape[-1] == H, f"x shape {tuple(x.shape)}")
     _req(x.dtype == (torch.float16 if xf else torch.bfloat16) and x.is_contiguous() and x.is_cuda, "x dtype / layout")
     _req(sel.dtype == torch.int64 and sel.is_contiguous() and sel.shape == (R, TOPK),
@@ -54,6 +55,7 @@ def forward(x, sel, rw, n_hot, gate_w, up_w, down_w, gate_s, up_s, down_s, act, 
 
 def gate_up(x, sel, rw, n_hot, gate_w, up_w, gate_s, up_s, act, gu32, ctr_a, blocks, lo, sh_gw=0, sh_uw=0, xf=0):
     """phase 1 of forward: act of the routed experts (and the shared expert)"""
+    on_device("moe4.gate_up", x, sel, rw, gate_w, up_w, gate_s, up_s, act, gu32, ctr_a)
     call("hmoe_moe4_gate_up", ptr(x), ptr(sel), ptr(rw), x.shape[0], int(n_hot), ptr(gate_w), ptr(up_w), ptr(gate_s),
          ptr(up_s), ptr(act), ptr(gu32), ptr(ctr_a), int(blocks), int(lo), _addr(sh_gw), _addr(sh_uw), int(xf),
          stream_of(x.device))
@@ -61,12 +63,14 @@ def gate_up(x, sel, rw, n_hot, gate_w, up_w, gate_s, up_s, act, gu32, ctr_a, blo
 
 def down(sel, rw, n_hot, down_w, down_s, act, y32, ctr_b, y, blocks, lo, sh_dw=0):
     """phase 2 of forward: y += down projections of act"""
+    on_device("moe4.down", y, sel, rw, down_w, down_s, act, y32, ctr_b)
     call("hmoe_moe4_down", ptr(sel), ptr(rw), sel.shape[0], int(n_hot), ptr(down_w), ptr(down_s), ptr(act), ptr(y32),
          ptr(ctr_b), ptr(y), int(blocks), int(lo), _addr(sh_dw), stream_of(y.device))
 
 
 def combine(f, o_ptr, y, rows, o2_ptr=0, done_ptr=0):
     """moe4.cu:817-824: f += y (+ o) (+ o2); y = 0"""
+    on_device("moe4.combine", f, y)
     _req(f.is_contiguous() and f.shape[-1] == H and f.dtype == torch.float32, "f")
     call("hmoe_moe4_combine", ptr(f), _addr(o_ptr), ptr(y), int(rows), _addr(o2_ptr), _addr(done_ptr),
          stream_of(f.device))
@@ -74,6 +78,7 @@ def combine(f, o_ptr, y, rows, o2_ptr=0, done_ptr=0):
 
 def dequant(q, sc, N, K):
     """moe4.cu:904-911: I4G128 codes + scales -> f16 [N, K]"""
+    on_device("moe4.dequant", q, sc)
     out = torch.empty((N, K), dtype=torch.float16, device=q.device)
     call("hmoe_moe4_dequant", ptr(q), ptr(sc), int(N), int(K), ptr(out), stream_of(q.device))
     return out
@@ -81,5 +86,6 @@ def dequant(q, sc, N, K):
 
 def finish_bf16(y, rows, out):
     """y fp32 [rows, H] -> bf16 out, y zeroed"""
+    on_device("finish_bf16", y, out)
     call("hmoe_finish_bf16", ptr(y), int(rows), ptr(out), stream_of(y.device))
     return out

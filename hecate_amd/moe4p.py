@@ -6,7 +6,7 @@ from a device-side dispatch plan (no host sync), and the shared expert in the sa
 """
 import torch
 
-from ._lib import call, lib, ptr, stream_of
+from ._lib import call, lib, on_device, ptr, stream_of
 
 H, I = 6144, 2048
 
@@ -26,6 +26,8 @@ def forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, inv=No
     """moe4p.cu:220-245: out[tok] += routed experts of the sorted picks (+ the shared expert on every token); x bf16, or
     its f16 copy (as router_fused writes it)"""
     T = x.shape[0]
+    on_device("moe4p", x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, inv, meta,
+              *(shared if shared is not None else ()))
     xf = 1 if x.dtype == torch.float16 else 0
     if not (x.dim() == 2 and x.shape[1] == H and x.dtype in (torch.bfloat16, torch.float16) and out.dtype == torch.float32
             and rbt.dim() == 2 and rbt.shape[1] == 4 and x.is_contiguous() and out.is_contiguous()):

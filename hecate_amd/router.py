@@ -5,7 +5,7 @@ router_fused(x, wt, bias, logits, ctr, sel, rw, topk, scale) keeps the reference
 """
 import torch
 
-from ._lib import call, lib, ptr, stream_of
+from ._lib import call, lib, on_device, ptr, stream_of
 
 
 def buffers(R, device, E=256):
@@ -16,6 +16,7 @@ def buffers(R, device, E=256):
 
 
 def router_fused(x, wt, bias, logits, ctr, sel, rw, topk, scale, xh=None):
+    on_device("router_fused", x, wt, bias, logits, ctr, sel, rw, xh)
     K = x.shape[-1]
     R = x.numel() // K
     E = wt.shape[0]
@@ -32,6 +33,7 @@ def norm_router(h, norm_w, eps, wt, logits, xn, xh=None):
     """nr4_kernel.cuh:122-381 (RMSNorm + router scores in one launch) for the decode path: xn = bf16 RMSNorm(h) * norm_w
     (bit-identical to hmoe_residual_rmsnorm without a residual add) and the router logits of xn into logits (the
     layout MoELayer.decode reads with phases=14); h fp32 [R, H], R <= 16"""
+    on_device("norm_router", h, norm_w, wt, logits, xn, xh)
     R, K = h.shape
     E = wt.shape[0]
     if not (h.dtype == torch.float32 and norm_w.dtype == torch.float32 and wt.dtype == torch.float32

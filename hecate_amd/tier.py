@@ -11,7 +11,7 @@ import numpy as np
 import torch
 
 from . import moe4, moe4p, router
-from ._lib import call, lib, ptr, stream_of
+from ._lib import call, lib, on_device, ptr, stream_of
 
 H, I, TOPK = 6144, 2048, 8
 I4_Q_GU, I4_S_GU = I * H // 2, I * (H // 128) * 2          # bytes of one gate / up matrix (codes, scales)
@@ -137,6 +137,7 @@ class PrefillBuffers:
         """device dispatch plan of a selection (tier_split.py:404-417 + pick_groups in one group), no host sync:
         counts, tok / eid / wt sorted by (expert, flat index), inv, rbt rows, meta = {npos, nrb, nrb wanted, 0}"""
         T = sel.shape[0]
+        on_device("dispatch", sel, rw, self.counts)
         if T > self.T:
             raise RuntimeError(f"dispatch: {T} rows > {self.T}")
         call("hmoe_dispatch", ptr(sel), ptr(rw), T, self.topk, self.lo, self.n, self.bm, int(bool(balance)),
@@ -198,6 +199,7 @@ class MoELayer:
         launches (1 router, 2 shared + routed gate/up, 4 shared + routed down, 8 output) for callers that time them
         apart"""
         R = x.shape[0]
+        on_device("decode", x, self.wg, y)
         if not (1 <= R <= 16 and x.dtype == torch.bfloat16 and x.is_contiguous() and x.shape[1] == H):
             raise RuntimeError("decode: x must be contiguous bf16 [R <= 16, 6144]")
         gq, uq, dq, gs, us, ds = self.bank.tables()
@@ -230,6 +232,7 @@ class MoELayer:
         """the prefill layer: bf16 [T, H] out (router, device dispatch plan, grouped GEMMs, per-token combine); an
         empty chunk gives an empty output (tier_split.py:377 returns out when no pick reaches the tier)"""
         T = x.shape[0]
+        on_device("prefill", x, self.wg)
         if T == 0:
             return torch.empty((0, H), dtype=torch.bfloat16, device=x.device)
         pf = self._prefill_buffers(T)

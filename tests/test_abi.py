@@ -37,6 +37,18 @@ def test_error_path_sets_message():
         _lib.call("hmoe_pack_i4", buf.ctypes.data, buf.ctypes.data, 15, 128, buf.ctypes.data, buf.ctypes.data)
 
 
+def test_host_tensors_are_refused():
+    """the Python operators refuse host tensors before any call into the library"""
+    import torch
+    from hecate_amd import moe4, router
+    x = torch.zeros(1, 6144, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="device"):
+        router.router_fused(x, torch.zeros(256, 6144), torch.zeros(256), torch.zeros(1), torch.zeros(1),
+                            torch.zeros(1, 8, dtype=torch.int64), torch.zeros(1, 8, dtype=torch.float16), 8, 2.5)
+    with pytest.raises(RuntimeError, match="device"):
+        moe4.finish_bf16(torch.zeros(1, 6144), 1, x)
+
+
 def test_empty_prefill_chunk_is_a_no_op():
     """no tokens and no picks: the prefill entry returns before any check of its buffers and before any GPU call
     (moe4p.cu:229 returns when no pick reaches the tier); tokens without buffers are still refused"""

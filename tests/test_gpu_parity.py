@@ -418,6 +418,20 @@ def test_prefill_empty_and_no_picks(dev):
     assert torch.equal(y, y0)
 
 
+def test_host_tensors_are_refused(dev):
+    """a host tensor among the arguments raises before any launch (its address would fault the kernel)"""
+    lay = gpu_layer("c2", dev, layer=0, bias_sigma=0.001, max_rows=2048)
+    x = synth.gen_x(3, 2, dev)
+    with pytest.raises(RuntimeError, match="device"):
+        lay.decode(x, y=torch.zeros(2, H))
+    with pytest.raises(RuntimeError, match="device"):
+        lay.prefill(x.cpu())
+    pf = lay._prefill_buffers(2)
+    with pytest.raises(RuntimeError, match="device"):
+        pf.run(pf.sel[:2].cpu(), pf.rw[:2])
+    assert lay.decode(x).shape == (2, H)                       # and the layer still serves device inputs
+
+
 @pytest.mark.parametrize("T", [1, 37, 300])
 def test_prefill_ragged(dev, T):
     """prefill chunks that are not a multiple of the 128-row block (the shared expert's last block partial, experts
