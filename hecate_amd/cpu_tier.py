@@ -12,8 +12,9 @@ import ctypes
 import time
 
 import numpy as np
+import torch
 
-from ._lib import call, ptr, stream_of
+from ._lib import call, on_device, ptr, stream_of
 
 H, I, TOPK, MAXR = 6144, 2048, 8, 8
 
@@ -91,6 +92,11 @@ class CpuTier:
         if not self.mapped:
             raise RuntimeError("cpu tier: submit needs the mapped mailbox")
         R = x.shape[0]
+        on_device("cpu tier submit", x, sel, rw)
+        if not (x.dtype == torch.bfloat16 and x.shape == (R, H) and sel.dtype == torch.int64 and sel.shape == (R, 8)
+                and rw.dtype == torch.float16 and rw.shape == (R, 8)
+                and x.is_contiguous() and sel.is_contiguous() and rw.is_contiguous()):
+            raise RuntimeError("cpu tier submit: x bf16 [R, H], sel int64 [R, 8], rw f16 [R, 8], contiguous")
         call("hmoe_cpu_submit", self.addr, ptr(x), ptr(sel), ptr(rw), int(R), int(layer),
              stream if stream is not None else stream_of(x.device))
         self._rows = R
@@ -98,6 +104,9 @@ class CpuTier:
     def collect(self, y, stream=None):
         """queue on the stream: wait for the pool, then y fp32 [R, H] += the CPU partial"""
         R = y.shape[0]
+        on_device("cpu tier collect", y)
+        if not (y.dtype == torch.float32 and y.dim() == 2 and y.shape[1] == H and y.is_contiguous()):
+            raise RuntimeError("cpu tier collect: y fp32 [R, H], contiguous")
         call("hmoe_cpu_collect", self.addr, ptr(y), int(R), stream if stream is not None else stream_of(y.device))
 
     def check(self):

@@ -21,6 +21,8 @@ class DecodeStack:
         if not 1 <= R <= 16:
             raise RuntimeError(f"DecodeStack: {R} rows")
         dev = layers[0].device
+        if len(norm_w) < len(layers) or any(w.device != dev or w.dtype != torch.float32 or w.numel() != H for w in norm_w):
+            raise RuntimeError("DecodeStack: one fp32 [H] norm weight per layer, on the layers' device")
         self.layers, self.norm_w, self.R, self.eps = layers, norm_w, R, eps
         self.x = torch.zeros((R, H), dtype=torch.bfloat16, device=dev)      # the step's input (static address)
         self.h = torch.zeros((R, H), dtype=torch.float32, device=dev)       # residual stream
