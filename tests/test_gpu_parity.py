@@ -397,6 +397,17 @@ def test_prefill_parity(dev):
     assert ma <= MAX_ABS and mr <= MEAN_REL
 
 
+def test_decode_bits_do_not_depend_on_the_grid(dev):
+    """the down kernel's part sums are fixed by (part, row block), not by how the items are spread over workgroups:
+    every allowed grid gives the same bits"""
+    lay = gpu_layer("c2", dev, layer=0, bias_sigma=0.001, max_rows=2048)
+    for R in (1, 4, 16):
+        x = synth.gen_x(40 + R, R, dev)
+        outs = [lay.decode(x, blocks=b).clone() for b in (0, 192, 240, 384)]
+        torch.cuda.synchronize()
+        assert all(torch.equal(outs[0], o) for o in outs[1:]), R
+
+
 def test_prefill_empty_and_no_picks(dev):
     """the reference's early returns (moe4p.cu:229 when no pick reaches the tier, tier_split.py:377): an empty chunk
     gives an empty output without an error, and a call with no picks and no shared expert leaves out untouched"""
