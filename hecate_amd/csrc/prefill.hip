@@ -396,11 +396,29 @@ extern "C" int hmoe_dispatch(const int64_t* sel, const uint16_t* rw, int T, int 
     return HMOE_LAUNCHED("dispatch");
 }
 
+// the gu scratch: the f16 copy of x ([T][H], when xf = 0) at 0, the shared expert's gate | up sums (fp32 [T][2I])
+// at SH_C_OFF, the library GEMMs' workspace (SH_WS bytes) after them
+constexpr size_t SH_WS = 32u << 20;
+#define SH_C_OFF(T) (((size_t) (T) * H * 2 + 255) & ~(size_t) 255)
+
+// act[t] = f16(silu(g) u) of the shared expert's sums (the dense case of the grouped GEMM's epilogue)
+__global__ void __launch_bounds__(256) sh_swiglu_kernel(const float* __restrict__ gu, int T, _Float16* __restrict__ act)
+{
+    const size_t i = ((size_t) blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= (size_t) T * I) return;
+    const size_t t = i / I, n = i - t * I;
+    const f32x4 g = *(const f32x4*) (gu + t * 2 * I + n), u = *(const f32x4*) (gu + t * 2 * I + I + n);
+    _Float16 o[4];
+    #pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = (_Float16) (silu(g[k]) * u[k]);
+    *(uint2*) (act + i) = *(const uint2*) o;
+}
+
 extern "C" size_t hmoe_moe4p_scratch_bytes(int which, int ps, int T)
 {
     switch (which)
     {
-        case 0: return (size_t) T * H * 2;                              // gu: the f16 copy of x (when xf = 0)
+        case 0: return SH_C_OFF(T) + (size_t) T * 2 * I * 4 + SH_WS;    // gu: x f16, shared g|u fp32, GEMM workspace
         case 1: return (size_t) (ps + T) * I * 2;                       // ar f16 [ps + T][I]
         case 2: return (size_t) (ps + T) * H * 4;                       // d fp32 [ps + T][H]
         default: return 0;
@@ -421,7 +439,8 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
                  "moe4p_forward: npos %d nrb %d ps %d T %d topk %d", npos, nrb, ps, T, topk);
     HMOE_REQUIRE(n_tab >= 0 && n_tab <= HMOE_MAXE && (n_tab == 0 || (gw && uw && dw && gs && us && ds)),
                  "moe4p_forward: tables");
-    HMOE_REQUIRE((!sh_gw && !sh_uw && !sh_dw) || (sh_gw && sh_uw && sh_dw && inv), "moe4p_forward: shared expert");
+    HMOE_REQUIRE((!sh_gw && !sh_uw && !sh_dw) || (sh_gw && sh_uw && sh_dw && inv && gu && ((uintptr_t) gu & 255) == 0),
+                 "moe4p_forward: the shared expert needs the inverse map and the gu scratch (256-byte aligned)");
     HMOE_REQUIRE(((uintptr_t) x & 15) == 0 && ((uintptr_t) ar & 15) == 0 && ((uintptr_t) d & 15) == 0 &&
                  ((uintptr_t) out & 15) == 0, "moe4p_forward: alignment");
     hipStream_t st = (hipStream_t) stream;
@@ -445,15 +464,17 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
     const bool sh = sh_gw != nullptr;
     if (sh)
     {
-        const int nbk = (T + PB - 1) / PB;
-        pgemm_kernel<true, 2, 2, 1><<<dim3(nbk, I / 128), PT, 0, st>>>((const _Float16*) xb, nullptr, nullptr, nullptr, 0, nullptr, 1,
-                                                                            nullptr, nullptr, nullptr, nullptr,
-                                                                            (const uint8_t*) sh_gw, (const uint8_t*) sh_uw,
-                                                                            a, nullptr, T, ps);
-        pgemm_kernel<true, 1, 4, 1><<<dim3(nbk, H / 256), PT, 0, st>>>(a, nullptr, nullptr,
-                                                                             nullptr, 0, nullptr, 1, nullptr, nullptr,
-                                                                             nullptr, nullptr, (const uint8_t*) sh_dw,
-                                                                             nullptr, nullptr, d, T, ps);
+        // the shared expert on every token: gate and up as library GEMMs into the fp32 sums [T][2I] of the gu scratch,
+        // act rows ps.. = f16(silu(g) u), then down into d rows ps.. (fp32) for the combine
+        uint8_t* scr = (uint8_t*) gu;
+        float* c = (float*) (scr + SH_C_OFF(T));
+        void* ws = scr + SH_C_OFF(T) + (size_t) T * 2 * I * 4;
+        const _Float16* xs = (const _Float16*) xb;
+        if (int rc = lt_gemm((const _Float16*) sh_gw, xs, c, I, T, H, 2 * I, ws, SH_WS, st)) return rc;
+        if (int rc = lt_gemm((const _Float16*) sh_uw, xs, c + I, I, T, H, 2 * I, ws, SH_WS, st)) return rc;
+        sh_swiglu_kernel<<<(unsigned) (((size_t) T * I / 4 + 255) / 256), 256, 0, st>>>(c, T, a + (size_t) ps * I);
+        if (int rc = lt_gemm((const _Float16*) sh_dw, a + (size_t) ps * I, d + (size_t) ps * H, H, T, I, H, ws, SH_WS, st))
+            return rc;
     }
     if (inv) pfin_kernel<<<T, 256, 0, st>>>(d, inv, topk, sh ? ps : -1, out);
     else if (npos > 0) pfin_atomic_kernel<<<npos, 256, 0, st>>>(d, tok, npos, meta, T, out);

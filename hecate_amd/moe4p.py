@@ -13,7 +13,7 @@ H, I = 6144, 2048
 
 def scratch(dev, npos, T=0):
     """moe4p.cu:209-215: [gu, ar, d] for up to npos picks (+ T rows for the shared expert); gu holds the f16 copy of
-    x when forward gets bf16 x"""
+    x when forward gets bf16 x, then (with the shared expert) its fp32 gate | up sums and the library GEMMs' workspace"""
     dev = torch.device(dev)
     L = lib()
     return [torch.zeros(int(L.hmoe_moe4p_scratch_bytes(0, npos, T)) // 4, dtype=torch.float32, device=dev),
@@ -28,6 +28,9 @@ def forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, inv=No
     T = x.shape[0]
     on_device("moe4p", x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, inv, meta,
               *(shared if shared is not None else ()))
+    if shared is not None and not all(w.dtype == torch.float16 and w.is_contiguous() and w.numel() == I * H
+                                      for w in shared):
+        raise RuntimeError("moe4p: the shared expert is row-major f16 gate [I, H], up [I, H], down [H, I]")
     xf = 1 if x.dtype == torch.float16 else 0
     if not (x.dim() == 2 and x.shape[1] == H and x.dtype in (torch.bfloat16, torch.float16) and out.dtype == torch.float32
             and rbt.dim() == 2 and rbt.shape[1] == 4 and x.is_contiguous() and out.is_contiguous()):
@@ -37,6 +40,13 @@ def forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, inv=No
     ps = ar.shape[0] - (T if shared is not None else 0)
     if npos > ps or d.shape[0] < ar.shape[0]:
         raise RuntimeError(f"moe4p: scratch holds {ps} picks, {npos} given")
+    # the scratch at least as large as the library writes it (a short one would be written past its end): gu holds
+    # the f16 copy of x when x is bf16, and the shared expert's sums and GEMM workspace when it is given
+    need = int(lib().hmoe_moe4p_scratch_bytes(0, ps, T)) if shared is not None else (T * H * 2 if xf == 0 else 0)
+    if need and (gu is None or gu.numel() * gu.element_size() < need):
+        raise RuntimeError(f"moe4p: the gu scratch needs {need} bytes")
+    if ar.dim() != 2 or ar.shape[1] != I or d.dim() != 2 or d.shape[1] != H:
+        raise RuntimeError("moe4p: ar f16 [rows, I] and d fp32 [rows, H]")
     sh = shared if shared is not None else (None, None, None)
     call("hmoe_moe4p_forward", ptr(x), ptr(tok), ptr(eid), ptr(wt), ptr(rbt), int(npos), int(nrb), gw.numel(),
          ptr(gw), ptr(uw), ptr(dw), ptr(gs), ptr(us), ptr(ds), ptr(gu), ptr(ar), ptr(d), ptr(out), int(ps),

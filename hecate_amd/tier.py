@@ -112,6 +112,12 @@ def load_reference_int4(u4dir, layer, experts, device):
     return bank
 
 
+def f16t_rows(t, N, K):
+    """an F16T matrix (1 KB tiles of 16 rows x 32 k, include/hecate_moe.h) as row-major f16 [N, K]: tile (nb, ks),
+    lane l = 16 j + r holds row 16 nb + r at k = 32 ks + 8 j .. + 8"""
+    return t.view(torch.float16).view(N // 16, K // 32, 4, 16, 8).permute(0, 3, 1, 2, 4).reshape(N, K).contiguous()
+
+
 class PrefillBuffers:
     """device buffers of a prefill chunk of up to T rows: selection, dispatch plan (hmoe_dispatch), GEMM scratch"""
 
@@ -166,6 +172,7 @@ class MoELayer:
         self.out = torch.zeros((self.max_rows, H), dtype=torch.bfloat16, device=dev)
         self.scr = moe4.scratch(dev)
         self._pf = None
+        self._shared_rows = None                                   # row-major copies of the shared expert (prefill)
 
     # ---- routing ---------------------------------------------------------------------------------------------
     def route(self, x, write_xh=True):
@@ -224,9 +231,17 @@ class MoELayer:
         T = x.shape[0]
         pf = self._pf
         gq, uq, dq, gs, us, ds = self.bank.tables()
-        sh = self.shared if (with_shared and self.shared is not None) else None
+        sh = self.shared_rows() if (with_shared and self.shared is not None) else None
         moe4p.forward(x, pf.tok, pf.eid, pf.wt, pf.rbt, gq, uq, dq, gs, us, ds, *pf.scr, y,
                       inv=pf.inv[:T * self.topk], meta=pf.meta, topk=self.topk, shared=sh, npos=pf.F, nrb=pf.nrb_max)
+
+    def shared_rows(self):
+        """the shared expert as row-major f16 (gate [I, H], up [I, H], down [H, I]) for the prefill's library GEMMs,
+        made from the F16T copies on first use"""
+        if self._shared_rows is None:
+            g, u, d = self.shared
+            self._shared_rows = (f16t_rows(g, I, H), f16t_rows(u, I, H), f16t_rows(d, H, I))
+        return self._shared_rows
 
     def prefill(self, x, with_shared=True):
         """the prefill layer: bf16 [T, H] out (router, device dispatch plan, grouped GEMMs, per-token combine); an

@@ -141,11 +141,15 @@ int hmoe_dispatch(const int64_t* sel, const uint16_t* rw, int T, int topk, int l
  * eid int32 [npos] (not read: the expert of a row block is in
  * rbt), wt fp32 [npos]; rbt int32 [nrb][4] rows {expert (relative to the tables), first pick, picks <= 128, 0};
  * tables (n_tab entries) as in hmoe_moe4_forward; ar f16 [ps + T][I] and d fp32 [ps + T][H] scratch
- * (hmoe_moe4p_scratch_bytes); gu: room for the f16 copy of x [T][H] when xf = 0 (else unused, NULL allowed); out
- * fp32 [T][H] accumulated into. meta: NULL, or the device
+ * (hmoe_moe4p_scratch_bytes); gu (256-byte aligned, hmoe_moe4p_scratch_bytes(0) bytes): the f16 copy of x [T][H]
+ * when xf = 0, then with the shared expert its fp32 gate | up sums [T][2I] and the library GEMMs' workspace (NULL
+ * allowed when xf = 1 and there is no shared expert); out fp32 [T][H] accumulated into. meta: NULL, or the device
  * {npos, nrb} written by hmoe_dispatch (then npos / nrb are the static maxima the grids are sized for). inv: NULL
  * (picks added with atomics, as p4_fin_kernel) or the dispatch's inverse map (each token's picks added in top-k
- * order: deterministic). sh_*: the shared expert as F16T or NULL (needs inv); it runs on every token with weight 1. */
+ * order: deterministic). sh_*: the shared expert as row-major f16 (gate [I][H], up [I][H], down [H][I]) or NULL
+ * (needs inv and gu); it runs on every token with weight 1, its projections as library GEMMs (hipBLASLt, fp32
+ * accumulation; a plan per token count is made on the first call with that count, so capture a graph after one eager
+ * call). T = 0 with npos = 0 is a no-op. */
 size_t hmoe_moe4p_scratch_bytes(int which, int ps, int T);     /* which: 0 gu, 1 ar, 2 d */
 int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid, const float* wt, const int* rbt, int npos,
                        int nrb, int n_tab, const int64_t* gw, const int64_t* uw, const int64_t* dw, const int64_t* gs,
