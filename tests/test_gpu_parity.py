@@ -443,6 +443,27 @@ def test_host_tensors_are_refused(dev):
     assert lay.decode(x).shape == (2, H)                       # and the layer still serves device inputs
 
 
+def test_prefill_replays_in_a_graph(dev):
+    """a prefill chunk (router, device dispatch plan, grouped GEMMs, the shared expert's library GEMMs, combine, bf16
+    out) captured once and replayed, with eager work and synchronisations between replays: every replay gives the
+    eager chunk's bits"""
+    log("prefill graph T=300")
+    lay = gpu_layer("c2", dev, layer=0, bias_sigma=0.001, max_rows=2048)
+    T = 300
+    x = synth.gen_x(77, T, dev)
+    ref = lay.prefill(x).clone()                              # eager (also sets up the library GEMM plans for T)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = lay.prefill(x)
+    for i in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), i
+        lay.decode(synth.gen_x(5 + i, 4, dev))
+        torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("T", [1, 37, 300])
 def test_prefill_ragged(dev, T):
     """prefill chunks that are not a multiple of the 128-row block (the shared expert's last block partial, experts
