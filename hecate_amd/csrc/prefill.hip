@@ -472,8 +472,16 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
         float* c = (float*) (scr + SH_C_OFF(T));
         void* ws = scr + SH_C_OFF(T) + (size_t) T * 2 * I * 4;
         const _Float16* xs = (const _Float16*) xb;
-        if (int rc = lt_gemm((const _Float16*) sh_gw, xs, c, I, T, H, 2 * I, ws, SH_WS, st)) return rc;
-        if (int rc = lt_gemm((const _Float16*) sh_uw, xs, c + I, I, T, H, 2 * I, ws, SH_WS, st)) return rc;
+        // (gate and up in one GEMM of 2I rows when up follows gate in memory)
+        if ((const _Float16*) sh_uw == (const _Float16*) sh_gw + (size_t) I * H)
+        {
+            if (int rc = lt_gemm((const _Float16*) sh_gw, xs, c, 2 * I, T, H, 2 * I, ws, SH_WS, st)) return rc;
+        }
+        else
+        {
+            if (int rc = lt_gemm((const _Float16*) sh_gw, xs, c, I, T, H, 2 * I, ws, SH_WS, st)) return rc;
+            if (int rc = lt_gemm((const _Float16*) sh_uw, xs, c + I, I, T, H, 2 * I, ws, SH_WS, st)) return rc;
+        }
         sh_swiglu_kernel<<<(unsigned) (((size_t) T * I / 4 + 255) / 256), 256, 0, st>>>(c, T, a + (size_t) ps * I);
         if (int rc = lt_gemm((const _Float16*) sh_dw, a + (size_t) ps * I, d + (size_t) ps * H, H, T, I, H, ws, SH_WS, st))
             return rc;

@@ -237,10 +237,12 @@ class MoELayer:
 
     def shared_rows(self):
         """the shared expert as row-major f16 (gate [I, H], up [I, H], down [H, I]) for the prefill's library GEMMs,
-        made from the F16T copies on first use"""
+        made from the F16T copies on first use; gate and up are the two halves of one [2I, H] matrix, so that the
+        library runs them as one GEMM"""
         if self._shared_rows is None:
             g, u, d = self.shared
-            self._shared_rows = (f16t_rows(g, I, H), f16t_rows(u, I, H), f16t_rows(d, H, I))
+            gu = torch.cat([f16t_rows(g, I, H), f16t_rows(u, I, H)])
+            self._shared_rows = (gu[:I], gu[I:], f16t_rows(d, H, I))
         return self._shared_rows
 
     def prefill(self, x, with_shared=True):
