@@ -114,7 +114,7 @@ __device__ __forceinline__ bool get_block(const int* rbt, int nrb, const int* me
 //   * each k step dequantises the 4 weight fragments (exact f16 codes times the f16 group scale) and runs the
 //     16x16x32 MFMA against the block's 16-pick tiles (up to 8).
 // DENSE: a dense F16T matrix over every token (block b = tokens [128 b, 128 b + 128), weight 1; groups of 4 tiles).
-// hmoe_moe4p_forward runs the shared expert as library GEMMs instead (shared_gemm.hip: 0.19 against 0.32 ms per
+// hmoe_moe4p_forward runs the shared expert as library GEMMs instead (shared_gemm.hip: 0.17 against 0.32 ms per
 // 2048-token chunk on this kernel), so no launch here instantiates it; it is kept as the library-free form.
 template <bool DENSE, int NMAT, int NS>
 struct PFetch
