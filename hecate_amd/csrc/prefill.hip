@@ -398,6 +398,8 @@ extern "C" int hmoe_dispatch(const int64_t* sel, const uint16_t* rw, int T, int 
     return HMOE_LAUNCHED("dispatch");
 }
 
+namespace hmoe {
+
 // the gu scratch: the f16 copy of x ([T][H], when xf = 0) at 0, the shared expert's gate | up sums (fp32 [T][2I])
 // at SH_C_OFF, the library GEMMs' workspace (SH_WS bytes) after them
 constexpr size_t SH_WS = 32u << 20;
@@ -415,6 +417,8 @@ __global__ void __launch_bounds__(256) sh_swiglu_kernel(const float* __restrict_
     for (int k = 0; k < 4; ++k) o[k] = (_Float16) (silu(g[k]) * u[k]);
     *(uint2*) (act + i) = *(const uint2*) o;
 }
+
+}  // namespace hmoe
 
 extern "C" size_t hmoe_moe4p_scratch_bytes(int which, int ps, int T)
 {
