@@ -91,6 +91,22 @@ def test_pack_dense_is_f16_tiles():
         assert t[nb, ks, l, e] == f16[nb * 16 + l % 16, ks * 32 + 8 * (l // 16) + e]
 
 
+def test_f16t_rows_inverts_pack_dense():
+    """tier.f16t_rows (the prefill's row-major copy of an F16T matrix) undoes hmoe_pack_dense element for element:
+    the result is the bf16 matrix's exact f16 values in row-major order"""
+    import torch
+    from hecate_amd import tier
+    rng = np.random.default_rng(5)
+    N, K = 48, 96
+    w = O.f32_to_bf16((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    out = np.empty(N * K, np.uint16)
+    _lib.call("hmoe_pack_dense", w.ctypes.data, N, K, out.ctypes.data)
+    rows = tier.f16t_rows(torch.from_numpy(out.view(np.int16)), N, K)
+    assert rows.shape == (N, K) and rows.dtype == torch.float16 and rows.is_contiguous()
+    f16 = O.bf16_to_f32(w).astype(np.float16).view(np.uint16)
+    assert np.array_equal(rows.view(torch.int16).numpy().view(np.uint16), f16)
+
+
 def test_repack_reference_moe4_weights():
     """tools/quant/gptq_int4.py:74-77 pack_u4 (the reference's fragment order, restated as a permutation of the
     code tensor) + fp32 row scales -> this build's I4G128: same codes, scale = bf16(row scale) in every group"""
