@@ -38,6 +38,11 @@ SIGNATURES = {
     "hmoe_moe4p_scratch_bytes": (sz, [i32, i32, i32]),
     "hmoe_moe4p_forward": (i32, [P, P, P, P, P, i32, i32, i32, P, P, P, P, P, P, P, P, P, P, i32, P, P, i32, i32,
                                  P, P, P, i32, P]),
+    "hmoe_shared_work_bytes": (sz, [i32]),
+    "hmoe_shared_forward": (i32, [P, i32, P, P, P, P, P, i32, P]),
+    "hmoe_moe4t_scratch_bytes": (sz, [i32, i32]),
+    "hmoe_moe4t_forward": (i32, [P, P, P, P, P, i32, i32, i32, P, P, P, P, P, P, P, P, P, P, i32, P, i32, i32, P]),
+    "hmoe_moe4t_gemm": (i32, [P, i32, P, i32, i32, P, P, P, P, P, i32, i32, P]),
     "hmoe_residual_rmsnorm": (i32, [P, P, P, i32, f32, P, P, P]),
     "hmoe_norm_router": (i32, [P, P, f32, i32, P, i32, P, P, P, P]),
     "hmoe_cpu_start": (i32, [P, i32, i32]),
@@ -96,6 +101,22 @@ def on_device(what, x, *ts):
     for t in ts:
         if t is not None and not isinstance(t, int) and getattr(t, "device", None) != dev:
             raise RuntimeError(f"{what}: every tensor must be on the device {dev}")
+
+
+XF_BF16, XF_FRAG, XF_F16 = 0, 1, 2      # the x format flags of include/hecate_moe.h
+
+
+def xf_of(x, xf=0):
+    """the C ABI's x format flag for a torch tensor passed with the reference's xf: xf = 0 means row-major x, read as
+    bf16 or fp16 by its dtype; xf = 1 (the reference's fragment-order x) is refused as the C ABI refuses it"""
+    import torch
+    if xf == XF_FRAG:
+        raise RuntimeError("xf=1 (the reference's B-fragment-order x) is not supported: pass row-major x")
+    if x.dtype == torch.bfloat16:
+        return XF_BF16
+    if x.dtype == torch.float16:
+        return XF_F16
+    raise RuntimeError(f"x must be bf16 or fp16, not {x.dtype}")
 
 
 def stream_of(device=None):

@@ -4,9 +4,10 @@ routing, add the CPU partial in tier_combine).
 
 CpuTier(threads) starts the pool on a mailbox. With mapped=True (the default) the mailbox is pinned, device-mapped
 host memory and the GPU drives the hand-off itself, one kernel each (so a hipGraph can hold them): submit() copies
-x / sel / rw into the mailbox and raises the flag, collect() waits (bounded) for the pool and adds the partial into y;
-check() reports a job's error once the stream has passed the collect. post() / wait() drive the
-same mailbox from the host (mapped=False needs no GPU), as tools/dev/test_grace_picks.py drives cpuband's flags.
+x / sel / rw into the mailbox and posts the next generation, collect() waits (bounded) for the pool to finish it and
+adds the partial into y; check() reports a job's error once the stream has passed the collect. post() / wait() drive
+the same mailbox from the host (mapped=False needs no GPU), as tools/dev/test_grace_picks.py drives cpuband's ISSUE /
+CPU_DONE generations.
 """
 import ctypes
 import time
@@ -21,9 +22,10 @@ H, I, TOPK, MAXR = 6144, 2048, 8, 8
 
 class Mailbox(ctypes.Structure):
     """hmoe_cpu_mailbox (include/hecate_moe.h)"""
-    _fields_ = [("pending", ctypes.c_int32), ("pad0", ctypes.c_int32 * 31),
+    _fields_ = [("issue", ctypes.c_uint32), ("pad0", ctypes.c_uint32 * 31),
+                ("done", ctypes.c_uint32), ("pad1", ctypes.c_uint32 * 31),
                 ("rows", ctypes.c_int32), ("layer", ctypes.c_int32), ("err", ctypes.c_int32),
-                ("gpu_err", ctypes.c_int32), ("pad1", ctypes.c_int32 * 28),
+                ("gpu_err", ctypes.c_int32), ("pad2", ctypes.c_int32 * 28),
                 ("sel", ctypes.c_int64 * (MAXR * TOPK)), ("rw", ctypes.c_uint16 * (MAXR * TOPK)),
                 ("x", ctypes.c_uint16 * (MAXR * H)), ("out", ctypes.c_float * (MAXR * H))]
 
@@ -63,24 +65,34 @@ class CpuTier:
 
     # ---- host-driven jobs ----
     def post(self, x_bf16, sel, rw_f16, layer):
-        """x bf16 bits u16 [R, H], sel int64 [R, 8], rw f16 bits u16 [R, 8]: fill the mailbox, then raise the flag"""
+        """x bf16 bits u16 [R, H], sel int64 [R, 8], rw f16 bits u16 [R, 8]: fill the mailbox, then post the next
+        generation (issue + 1); returns it"""
         x_bf16 = np.ascontiguousarray(x_bf16, np.uint16)
         R = x_bf16.shape[0]
         if not 1 <= R <= MAXR or x_bf16.shape[1] != H:
             raise RuntimeError(f"cpu tier: {R} rows")
-        if self.mb.pending:
+        if self.mb.done != self.mb.issue:
             raise RuntimeError("cpu tier: a job is in flight")
         ctypes.memmove(self.mb.x, x_bf16.ctypes.data, x_bf16.nbytes)
         ctypes.memmove(self.mb.sel, np.ascontiguousarray(sel, np.int64).ctypes.data, R * TOPK * 8)
         ctypes.memmove(self.mb.rw, np.ascontiguousarray(rw_f16, np.uint16).ctypes.data, R * TOPK * 2)
         self.mb.rows, self.mb.layer, self.mb.err = R, int(layer), 0
-        self.mb.pending = 1                      # (x86 stores are seen in order: the job before the flag)
-        self._rows = R
+        return self.raise_issue(R)
 
-    def wait(self, timeout=60.0):
-        """wait for the pool to lower the flag; the partial fp32 [R, H] (a copy) and the job's err"""
+    def raise_issue(self, rows):
+        """post the next generation over whatever job the mailbox holds (x86 stores are seen in order: the job before
+        the generation); returns it"""
+        g = (int(self.mb.issue) + 1) & 0xFFFFFFFF or 1            # (0 is skipped on wrap-around)
+        self.mb.issue = g
+        self._rows, self._gen = rows, g
+        return g
+
+    def wait(self, timeout=60.0, gen=None):
+        """wait until the pool has finished generation gen (default: the last one posted here); the partial fp32
+        [R, H] (a copy) and the job's err. Any other value of done (an older job, a stale number) does not end it"""
         t0 = time.perf_counter()
-        while self.mb.pending:
+        want = self._gen if gen is None else gen
+        while self.mb.done != want:
             if time.perf_counter() - t0 > timeout:
                 raise RuntimeError("cpu tier: the job did not finish")
         out = np.ctypeslib.as_array(self.mb.out)[:self._rows * H].reshape(self._rows, H).copy()

@@ -14,9 +14,12 @@
 // the thread count.
 #include "hecate_moe.h"
 
+#include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <immintrin.h>
@@ -60,8 +63,12 @@ struct Pool
     std::vector<Layer> layers;
     hmoe_cpu_mailbox* mb = nullptr;
     std::atomic<int> stop{0};
-    std::atomic<int> bar_count{0}, bar_gen{0};
+    alignas(128) std::atomic<int> bar_count{0};      // (counter and generation on their own lines)
+    alignas(128) std::atomic<int> bar_gen{0};
     int nthr = 0;
+    uint32_t start_gen = 0;                           // the mailbox's issue at start: taken as served
+    bool skip = false;                                // HMOE_CPU_SKIP: acknowledge jobs with a zero partial
+    int hold_t = -1, hold_us = 0;                     // HMOE_CPU_HOLD test hook
     Work w;
     std::atomic<long long> jobs{0}, picks{0};
 };
@@ -69,17 +76,23 @@ struct Pool
 static Pool* g_pool = nullptr;
 static std::mutex g_mu;
 
-// barrier for the pool's threads (sense by generation)
-static void barrier(Pool& p)
+// barrier for the pool's threads (sense by generation); false when the pool is stopping (a thread that never arrives,
+// e.g. one held back or gone, must not keep the others here past hmoe_cpu_stop)
+static bool barrier(Pool& p)
 {
     const int gen = p.bar_gen.load(std::memory_order_acquire);
     if (p.bar_count.fetch_add(1, std::memory_order_acq_rel) + 1 == p.nthr)
     {
         p.bar_count.store(0, std::memory_order_relaxed);
         p.bar_gen.store(gen + 1, std::memory_order_release);
+        return true;
     }
-    else
-        while (p.bar_gen.load(std::memory_order_acquire) == gen) _mm_pause();
+    while (p.bar_gen.load(std::memory_order_acquire) == gen)
+    {
+        if (p.stop.load(std::memory_order_acquire)) return false;
+        _mm_pause();
+    }
+    return true;
 }
 
 // q8_0 of a 32-element group
@@ -223,8 +236,8 @@ static void range(int total, int t, int T, int& a, int& b)
     b = (int) ((long long) total * (t + 1) / T);
 }
 
-// one job, by every thread of the pool (t = 0 .. nthr - 1)
-static void run_job(Pool& p, int t)
+// one job (generation g), by every thread of the pool (t = 0 .. nthr - 1); false when the pool stopped inside it
+static bool run_job(Pool& p, int t, uint32_t g)
 {
     hmoe_cpu_mailbox* mb = p.mb;
     Work& w = p.w;
@@ -234,7 +247,7 @@ static void run_job(Pool& p, int t)
         const int R = mb->rows, L = mb->layer;
         w.R = (R >= 1 && R <= CMAXR) ? R : 0;
         w.P = 0;
-        if (w.R && L >= 0 && L < (int) p.layers.size())
+        if (w.R && !p.skip && L >= 0 && L < (int) p.layers.size())
         {
             const Layer& ly = p.layers[L];
             const int n = (int) ly.ex.size();
@@ -255,7 +268,7 @@ static void run_job(Pool& p, int t)
             }
         }
     }
-    barrier(p);
+    if (!barrier(p)) return false;
     const int R = w.R, P = w.P;
     const Layer* ly = (R && mb->layer >= 0 && mb->layer < (int) p.layers.size()) ? &p.layers[mb->layer] : nullptr;
     // q8_0 of every row of x
@@ -269,7 +282,7 @@ static void run_job(Pool& p, int t)
             quant_group(v, w.xq.data() + (size_t) gi * 32, w.xs.data() + gi);
         }
     }
-    barrier(p);
+    if (!barrier(p)) return false;
     // per pick: gate / up over the pick's rows, then act -> q8_0
     static thread_local std::vector<int8_t> xqp(CMAXR * H);
     static thread_local std::vector<float> xsp(CMAXR * H / 32);
@@ -287,7 +300,7 @@ static void run_job(Pool& p, int t)
         range(I, t, T, a, b);
         gemv_any(ex.gate, H, xqp.data(), xsp.data(), nr, a, b, w.gy.data(), I);
         gemv_any(ex.up, H, xqp.data(), xsp.data(), nr, a, b, w.uy.data(), I);
-        barrier(p);
+        if (!barrier(p)) return false;
         range(nr * I / 32, t, T, a, b);
         for (int gi = a; gi < b; ++gi)
         {
@@ -302,7 +315,7 @@ static void run_job(Pool& p, int t)
             quant_group(v, w.aq.data() + ((size_t) q * CMAXR + j) * I + k0,
                         w.as.data() + (((size_t) q * CMAXR + j) * I + k0) / 32);
         }
-        barrier(p);
+        if (!barrier(p)) return false;
     }
     // down: output rows split over the threads, picks in order, summed into out from 0
     {
@@ -323,14 +336,15 @@ static void run_job(Pool& p, int t)
             }
         }
     }
-    barrier(p);
+    if (!barrier(p)) return false;
     if (t == 0)
     {
         p.jobs.fetch_add(1, std::memory_order_relaxed);
         p.picks.fetch_add(P, std::memory_order_relaxed);
-        mb->err = !R ? 1 : (ly ? 0 : 2);                   // 1: bad row count, 2: no such layer
-        __atomic_store_n(&mb->pending, 0, __ATOMIC_RELEASE);
+        mb->err = !R ? 1 : (ly || p.skip ? 0 : 2);          // 1: bad row count, 2: no such layer
+        __atomic_store_n(&mb->done, g, __ATOMIC_RELEASE);
     }
+    return true;
 }
 
 static void worker(Pool* p, int t, int core)
@@ -343,18 +357,23 @@ static void worker(Pool* p, int t, int core)
         sched_setaffinity(0, sizeof(cs), &cs);       // best effort
     }
     int idle = 0;
+    uint32_t last = p->start_gen;                    // the generation this thread served last
     while (true)
     {
-        // every thread watches the flag; all see the same job because the flag is cleared only after the job's last
-        // barrier, which every thread passes
+        // every thread watches issue and runs each generation once: a poster may post the next job only when done
+        // equals issue, and done is written after the job's last barrier, which every thread passes, so no thread can
+        // miss a generation or see a job's inputs change under it (the 0/1 flag this replaces let a slow thread take a
+        // re-raised flag for the job it had just finished)
         if (p->stop.load(std::memory_order_acquire)) return;
-        if (__atomic_load_n(&p->mb->pending, __ATOMIC_ACQUIRE) == 1)
+        const uint32_t g = __atomic_load_n(&p->mb->issue, __ATOMIC_ACQUIRE);
+        if (g != last)
         {
             idle = 0;
-            run_job(*p, t);
-            // wait until thread 0 has cleared the flag before looking for the next job
-            while (__atomic_load_n(&p->mb->pending, __ATOMIC_ACQUIRE) == 1 && !p->stop.load(std::memory_order_acquire))
-                _mm_pause();
+            last = g;
+            if (!run_job(*p, t, g)) return;
+            if (t == p->hold_t)
+                for (int us = 0; us < p->hold_us && !p->stop.load(std::memory_order_acquire); us += 1000)
+                    std::this_thread::sleep_for(std::chrono::microseconds(std::min(1000, p->hold_us - us)));
             continue;
         }
         if (++idle < 4096) _mm_pause();
@@ -381,7 +400,12 @@ extern "C" int hmoe_cpu_start(hmoe_cpu_mailbox* mb, int threads, int first_core)
     Pool* p = new Pool();
     p->mb = mb;
     p->nthr = threads;
-    mb->pending = 0;
+    p->start_gen = __atomic_load_n(&mb->issue, __ATOMIC_ACQUIRE);
+    __atomic_store_n(&mb->done, p->start_gen, __ATOMIC_RELEASE);     // nothing in flight
+    const char* skip = std::getenv("HMOE_CPU_SKIP");
+    p->skip = skip && std::atoi(skip) != 0;
+    if (const char* hold = std::getenv("HMOE_CPU_HOLD"))
+        if (std::sscanf(hold, "%d,%d", &p->hold_t, &p->hold_us) != 2) p->hold_t = -1;
     g_pool = p;
     for (int t = 0; t < threads; ++t) p->th.emplace_back(worker, p, t, first_core >= 0 ? first_core + t : -1);
     return 0;
@@ -392,9 +416,13 @@ extern "C" int hmoe_cpu_add_layer(int layer, int lo, int n, const uint8_t* const
     std::lock_guard<std::mutex> lk(g_mu);
     if (!g_pool) return hmoe::set_error(HMOE_ERR_ARG, "cpu_add_layer: no pool");
     if (layer < 0 || layer > 4096 || lo < 0 || n < 0 || n > 256 || (n && (!q || !s))) return hmoe::set_error(HMOE_ERR_ARG, "cpu_add_layer: arguments");
-    if (__atomic_load_n(&g_pool->mb->pending, __ATOMIC_ACQUIRE)) return hmoe::set_error(HMOE_ERR_ARG, "cpu_add_layer: a job is in flight");
-    if ((int) g_pool->layers.size() <= layer) g_pool->layers.resize(layer + 1);
-    Layer& L = g_pool->layers[layer];
+    hmoe_cpu_mailbox* mb = g_pool->mb;
+    if (__atomic_load_n(&mb->issue, __ATOMIC_ACQUIRE) != __atomic_load_n(&mb->done, __ATOMIC_ACQUIRE))
+        return hmoe::set_error(HMOE_ERR_ARG, "cpu_add_layer: a job is in flight");
+    // every pointer is checked before the pool's layers change
+    for (int i = 0; i < 3 * n; ++i)
+        if (!q[i] || !s[i]) return hmoe::set_error(HMOE_ERR_ARG, "cpu_add_layer: null matrix (expert %d)", i / 3);
+    Layer L;
     L.lo = lo;
     L.ex.assign(n, Expert{});
     for (int e = 0; e < n; ++e)
@@ -403,9 +431,9 @@ extern "C" int hmoe_cpu_add_layer(int layer, int lo, int n, const uint8_t* const
         L.ex[e].gate = {q[3 * e + 0], s[3 * e + 0]};
         L.ex[e].up = {q[3 * e + 1], s[3 * e + 1]};
         L.ex[e].down = {q[3 * e + 2], s[3 * e + 2]};
-        for (int k = 0; k < 3; ++k)
-            if (!q[3 * e + k] || !s[3 * e + k]) return hmoe::set_error(HMOE_ERR_ARG, "cpu_add_layer: null matrix");
     }
+    if ((int) g_pool->layers.size() <= layer) g_pool->layers.resize(layer + 1);
+    g_pool->layers[layer] = std::move(L);
     return 0;
 }
 

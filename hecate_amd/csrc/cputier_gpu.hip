@@ -11,12 +11,17 @@
 
 namespace hmoe {
 
-// thread 0 polls the flag until it reads `want` or `ticks` wall-clock ticks pass; true when it read `want`
-__device__ bool wait_flag(const int32_t* flag, int want, long long ticks)
+__device__ __forceinline__ uint32_t load_sys(const uint32_t* p)
+{
+    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// thread 0 polls the pool's done generation until it equals `want` or `ticks` wall-clock ticks pass; true when it did
+__device__ bool wait_done(const hmoe_cpu_mailbox* mb, uint32_t want, long long ticks)
 {
     const long long t0 = wall_clock64();
     for (;;) {
-        if (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) == want) return true;
+        if (load_sys(&mb->done) == want) return true;
         if (wall_clock64() - t0 > ticks) return false;
         __builtin_amdgcn_s_sleep(16);
     }
@@ -28,10 +33,13 @@ __global__ void __launch_bounds__(1024) cpu_handoff_kernel(const uint4* __restri
                                                            int layer, long long ticks)
 {
     __shared__ int ready;
+    __shared__ uint32_t gen;
     if (threadIdx.x == 0) {
         // the previous job is done (its collect waited for it, unless that wait ran out)
-        ready = wait_flag(&mb->pending, 0, ticks);
+        const uint32_t g = load_sys(&mb->issue);
+        ready = wait_done(mb, g, ticks);
         if (!ready) __hip_atomic_store(&mb->gpu_err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        gen = g + 1u == 0u ? 1u : g + 1u;                       // (0 is skipped on wrap-around)
     }
     __syncthreads();
     if (!ready) return;
@@ -49,17 +57,20 @@ __global__ void __launch_bounds__(1024) cpu_handoff_kernel(const uint4* __restri
     // each wave's mailbox stores reach the host before the barrier, the flag after it
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
     __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_store(&mb->pending, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (threadIdx.x == 0) __hip_atomic_store(&mb->issue, gen, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-// one workgroup per row: y[r] += out[r] once the pool has lowered the flag
+// one workgroup per row: y[r] += out[r] once the pool has finished the generation the hand-off posted (issue); with
+// gpu_err set (a hand-off that found the pool busy posted nothing) the partial in the mailbox is not this step's, and
+// nothing is added
 __global__ void __launch_bounds__(256) cpu_collect_kernel(const hmoe_cpu_mailbox* mb, float* __restrict__ y,
                                                           int32_t* gpu_err, long long ticks)
 {
     __shared__ int done;
     if (threadIdx.x == 0) {
-        done = wait_flag(&mb->pending, 0, ticks);
-        if (!done) __hip_atomic_store(gpu_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        const int e0 = __hip_atomic_load(gpu_err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        done = e0 == 0 && wait_done(mb, load_sys(&mb->issue), ticks);
+        if (!done && e0 == 0) __hip_atomic_store(gpu_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
     __syncthreads();
     if (!done) return;

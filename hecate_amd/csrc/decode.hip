@@ -622,6 +622,10 @@ struct DecodeArgs
 
 static int check(const DecodeArgs& a)
 {
+    // a.xf: 0 bf16, 1 fp16 (mapped from HMOE_XF_BF16 / HMOE_XF_F16); -1 any other flag, the reference's fragment-order
+    // x (HMOE_XF_FRAG) included
+    HMOE_REQUIRE(a.xf == 0 || a.xf == 1, "moe4: xf must be HMOE_XF_BF16 (0) or HMOE_XF_F16 (2); the reference's "
+                 "fragment-order x (xf = 1) is not supported, pass row-major x");
     HMOE_REQUIRE(a.R >= 1 && a.R <= MAXR, "moe4: rows %d not in [1, %d]", a.R, MAXR);
     HMOE_REQUIRE(a.n_hot >= 0 && a.n_hot <= HMOE_MAXE && a.lo >= 0, "moe4: window lo %d n_hot %d", a.lo, a.n_hot);
     HMOE_REQUIRE(a.x && a.act && a.ctr && a.y32, "moe4: null buffer");
@@ -696,7 +700,7 @@ static DecodeArgs forward_args(const void* x, const int64_t* sel, const uint16_t
                                const void* sh_uw, const void* sh_dw, int xf)
 {
     DecodeArgs a = {};
-    a.x = x; a.xf = xf; a.sel_in = sel; a.rw_in = rw; a.R = R; a.n_hot = n_hot; a.lo = lo;
+    a.x = x; a.xf = xf == HMOE_XF_F16 ? 1 : xf == HMOE_XF_BF16 ? 0 : -1; a.sel_in = sel; a.rw_in = rw; a.R = R; a.n_hot = n_hot; a.lo = lo;
     a.gate_w = gate_w; a.up_w = up_w; a.down_w = down_w; a.gate_s = gate_s; a.up_s = up_s; a.down_s = down_s;
     a.act = (_Float16*) act; a.ctr = ctr_a; a.y32 = y32; a.y = y; a.out = nullptr;
     a.sh_gw = sh_gw; a.sh_uw = sh_uw; a.sh_dw = sh_dw; a.blocks = blocks;
@@ -723,7 +727,7 @@ extern "C" int hmoe_moe4_down(const int64_t* sel, const uint16_t* rw, int R, int
 {
     // ctr_b holds the part count handed from the down launch to the reduction (ctr_a of forward)
     DecodeArgs a = forward_args(act, sel, rw, R, n_hot, down_w, down_w, down_w, down_s, down_s, down_s, (void*) act,
-                                ctr_b, y32, y, blocks, lo, sh_dw, sh_dw, sh_dw, 1);
+                                ctr_b, y32, y, blocks, lo, sh_dw, sh_dw, sh_dw, HMOE_XF_F16);
     int rc = check(a);
     if (rc) return rc;
     HMOE_REQUIRE(sel && rw && y, "moe4_down: null buffer");
@@ -773,7 +777,7 @@ extern "C" int hmoe_moe_decode_layer(const void* x, const float* wt, const float
     HMOE_REQUIRE(y || out, "decode_layer: no output");
     HMOE_REQUIRE(phases >= 1 && phases <= 15, "decode_layer: phases %d", phases);
     DecodeArgs a = forward_args(x, nullptr, nullptr, R, n_hot, gate_w, up_w, down_w, gate_s, up_s, down_s, act, ctr_a,
-                                y32, y, blocks, lo, sh_gw, sh_uw, sh_dw, 0);
+                                y32, y, blocks, lo, sh_gw, sh_uw, sh_dw, HMOE_XF_BF16);
     a.wt = wt; a.bias = bias; a.logits = logits; a.E = E; a.topk = topk; a.scale = scale; a.sel_out = sel;
     a.rw_out = rw; a.out = out;
     int rc = check(a);

@@ -95,11 +95,12 @@ __global__ void __launch_bounds__(DBLK) disp_place_kernel(const int64_t* __restr
 // ---------------------------------------------------------------------------------------------------------------
 struct Block { int e, p0, rows; };
 
+// row block blockIdx.x of the plan: up to 2 PB picks (the dispatch's bm <= 256), run as halves of <= PB picks
 __device__ __forceinline__ bool get_block(const int* rbt, int nrb, const int* meta, int n_tab, Block& b)
 {
     const int rb = blockIdx.x;
     if (rb >= nrb || (meta && rb >= meta[1])) return false;
-    b.e = rbt[4 * rb]; b.p0 = rbt[4 * rb + 1]; b.rows = min(rbt[4 * rb + 2], PB);
+    b.e = rbt[4 * rb]; b.p0 = rbt[4 * rb + 1]; b.rows = min(rbt[4 * rb + 2], 2 * PB);
     return b.e >= 0 && b.e < n_tab && b.rows > 0;
 }
 
@@ -123,14 +124,20 @@ struct PFetch
     uint16_t s[NS][NMAT];
 };
 
-template <bool DENSE, int NMAT, int NS, int D>
+// epilogues: gate/up -> act f16 (EPI_ACT) or the raw gate and up sums (EPI_RAW, fp32 [2][ps][I], the test entry of
+// moe4t); down -> d fp32 rows (EPI_D) or added into out[tok] with fp32 atomics (EPI_FIN, moe4t.cu's down epilogue)
+enum { EPI_ACT = 0, EPI_RAW = 1, EPI_D = 2, EPI_FIN = 3 };
+
+template <bool DENSE, int NMAT, int NS, int D, int EPI = NMAT == 2 ? EPI_ACT : EPI_D>
 __global__ void __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(2))) pgemm_kernel(
     const _Float16* __restrict__ xin, const int* __restrict__ tok, const float* __restrict__ wt,
     const int* __restrict__ rbt, int nrb, const int* __restrict__ meta, int n_tab,
     const int64_t* __restrict__ w0, const int64_t* __restrict__ w1, const int64_t* __restrict__ s0,
     const int64_t* __restrict__ s1, const uint8_t* __restrict__ dense0, const uint8_t* __restrict__ dense1,
-    _Float16* __restrict__ ar, float* __restrict__ dout, int T, int off)
+    _Float16* __restrict__ ar, float* __restrict__ dout, int T, int off, float* __restrict__ fout = nullptr,
+    int ps = 0)
 {
+    static_assert((NMAT == 2) == (EPI == EPI_ACT || EPI == EPI_RAW), "gate/up epilogues need both matrices");
     constexpr int K = NMAT == 2 ? H : I;                 // gate/up: x [T][H] -> act; down: act [.][I] -> d
     constexpr int NOUT = NMAT == 2 ? I : H;
     constexpr int KG = K / 128, KS = K / 32;
@@ -141,164 +148,190 @@ __global__ void __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(2))) pg
     // as one contiguous 1 KB wave read (no bank conflicts); two buffers, the next group loads while one computes
     __shared__ __attribute__((aligned(16))) u32x4 xs0[32 * 64];
     __shared__ __attribute__((aligned(16))) u32x4 xs1[32 * 64];
-    Block b;
-    if (DENSE) { b.e = 0; b.p0 = blockIdx.x * PB; b.rows = min(PB, T - b.p0); if (b.rows <= 0) return; }
-    else if (!get_block(rbt, nrb, meta, n_tab, b)) return;
-    const int t = threadIdx.x, l = t & 63, row = l & 15;
-    const int w = __builtin_amdgcn_readfirstlane(t >> 6);   // wave index, kept in a scalar register
-    const int nb0 = (blockIdx.y * 4 + w) * NS;
-    const uint8_t* wp[NMAT];
-    const uint8_t* sp[NMAT];
-    #pragma unroll
-    for (int m = 0; m < NMAT; ++m)
+    Block rb;
+    if (DENSE) { rb.e = 0; rb.p0 = blockIdx.x * PB; rb.rows = min(PB, T - rb.p0); if (rb.rows <= 0) return; }
+    else if (!get_block(rbt, nrb, meta, n_tab, rb)) return;
+    // a block of more than PB picks runs as two halves, one after the other (the second reads the weights again,
+    // mostly from the caches); the barrier between them keeps the first half's last LDS reads ahead of the second
+    // half's first staging
+    for (int h0 = 0; h0 < rb.rows; h0 += PB)
     {
-        wp[m] = DENSE ? (m == 0 ? dense0 : dense1) : (const uint8_t*) (m == 0 ? w0 : w1)[b.e];
-        sp[m] = DENSE ? nullptr : (const uint8_t*) (m == 0 ? s0 : s1)[b.e];
-    }
-    const int ntt = (b.rows + 15) >> 4;
-    const DqConsts dq = dq_consts();
-    // wave w stages tiles 2w and 2w + 1: lane l's source row; a pick past the block re-reads a valid row (its output
-    // columns are never stored), a whole tile past the block reads one fixed 16 bytes
-    const _Float16* src[2];
-    #pragma unroll
-    for (int h = 0; h < 2; ++h)
-    {
-        const int tt = 2 * w + h, pk = tt * 16 + row;
-        const bool in = pk < b.rows, tin = tt < ntt;
-        int srow;
-        if (NMAT == 2)
+        if (h0) __syncthreads();
+        const Block b = {rb.e, rb.p0 + h0, min(PB, rb.rows - h0)};
+        const int t = threadIdx.x, l = t & 63, row = l & 15;
+        const int w = __builtin_amdgcn_readfirstlane(t >> 6);   // wave index, kept in a scalar register
+        const int nb0 = (blockIdx.y * 4 + w) * NS;
+        const uint8_t* wp[NMAT];
+        const uint8_t* sp[NMAT];
+        #pragma unroll
+        for (int m = 0; m < NMAT; ++m)
         {
-            const int tk = DENSE ? b.p0 + (in ? pk : 0) : tok[b.p0 + (in ? pk : 0)];
-            srow = (unsigned) tk < (unsigned) T ? tk : 0;
+            wp[m] = DENSE ? (m == 0 ? dense0 : dense1) : (const uint8_t*) (m == 0 ? w0 : w1)[b.e];
+            sp[m] = DENSE ? nullptr : (const uint8_t*) (m == 0 ? s0 : s1)[b.e];
         }
-        else srow = off + b.p0 + (in ? pk : 0);
-        src[h] = xin + (size_t) srow * K + (tin ? 8 * (l >> 4) : 0);
-    }
-    // Direct global-to-LDS loads (16 bytes per lane, lane l at LDS base + 16 l), issued from inline assembly: the
-    // compiler then does not count them, so its own waits for the weight ring stay exact, and the wait that makes a
-    // staged group visible is placed by hand before the barrier (the loads issued after a stage are exactly the
-    // FETCH_LOADS of one ring refill). M0 holds the LDS base of each load; nothing else in this kernel uses M0.
-    constexpr int FETCH_LOADS = DENSE ? NS * NMAT * 4 : NS * NMAT * 2;
-    auto stage = [&](int kg, u32x4* buf) {
+        const int ntt = (b.rows + 15) >> 4;
+        const DqConsts dq = dq_consts();
+        // wave w stages tiles 2w and 2w + 1: lane l's source row; a pick past the block re-reads a valid row (its output
+        // columns are never stored), a whole tile past the block reads one fixed 16 bytes
+        const _Float16* src[2];
         #pragma unroll
         for (int h = 0; h < 2; ++h)
         {
-            const int tt = 2 * w + h;
-            const bool tin = tt < ntt;
-            #pragma unroll
-            for (int k = 0; k < 4; ++k)
+            const int tt = 2 * w + h, pk = tt * 16 + row;
+            const bool in = pk < b.rows, tin = tt < ntt;
+            int srow;
+            if (NMAT == 2)
             {
-                const _Float16* gp = src[h] + (tin ? kg * 128 + 32 * k : 0);
-                const uint32_t lds = __builtin_amdgcn_readfirstlane(
-                    (uint32_t) (uintptr_t) (__attribute__((address_space(3))) void*) (buf + (tt * 4 + k) * 64));
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-                asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(gp), "s"(lds) : "memory", "m0");
-#pragma clang diagnostic pop
+                // (no token map: the picks' inputs are rows p0 .. of xin, as the moe4t test entry passes them)
+                const int tk = (DENSE || !tok) ? b.p0 + (in ? pk : 0) : tok[b.p0 + (in ? pk : 0)];
+                srow = (unsigned) tk < (unsigned) T ? tk : 0;
             }
+            else srow = off + b.p0 + (in ? pk : 0);
+            src[h] = xin + (size_t) srow * K + (tin ? 8 * (l >> 4) : 0);
         }
-    };
-    PFetch<DENSE, NMAT, NS> ring[D];
-    auto fetch = [&](int kg, auto sc) {
-        constexpr int s = decltype(sc)::value;
-        #pragma unroll
-        for (int st = 0; st < NS; ++st)
+        // Direct global-to-LDS loads (16 bytes per lane, lane l at LDS base + 16 l), issued from inline assembly: the
+        // compiler then does not count them, so its own waits for the weight ring stay exact, and the wait that makes a
+        // staged group visible is placed by hand before the barrier (the loads issued after a stage are exactly the
+        // FETCH_LOADS of one ring refill). M0 holds the LDS base of each load; nothing else in this kernel uses M0.
+        constexpr int FETCH_LOADS = DENSE ? NS * NMAT * 4 : NS * NMAT * 2;
+        auto stage = [&](int kg, u32x4* buf) {
             #pragma unroll
-            for (int m = 0; m < NMAT; ++m)
+            for (int h = 0; h < 2; ++h)
             {
-                const int nb = nb0 + st;
-                if (DENSE)
+                const int tt = 2 * w + h;
+                const bool tin = tt < ntt;
+                #pragma unroll
+                for (int k = 0; k < 4; ++k)
                 {
-                    #pragma unroll
-                    for (int u = 0; u < 4; ++u) ring[s].q[st][m][u] = ldw16(wp[m] + ((size_t) (nb * KS + kg * 4 + u) * 64 + l) * 16);
-                }
-                else
-                {
-                    ring[s].q[st][m][0] = ldw16(wp[m] + ((size_t) (nb * KG + kg) * 64 + l) * 16);
-                    ring[s].s[st][m] = ldg<uint16_t>(sp[m] + ((size_t) (nb * 16 + row) * KG + kg) * 2);
+                    const _Float16* gp = src[h] + (tin ? kg * 128 + 32 * k : 0);
+                    const uint32_t lds = __builtin_amdgcn_readfirstlane(
+                        (uint32_t) (uintptr_t) (__attribute__((address_space(3))) void*) (buf + (tt * 4 + k) * 64));
+    #pragma clang diagnostic push
+    #pragma clang diagnostic ignored "-Winline-asm"
+                    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(gp), "s"(lds) : "memory", "m0");
+    #pragma clang diagnostic pop
                 }
             }
-    };
-    f32x4 acc[NS][NMAT][8];
-    #pragma unroll
-    for (int st = 0; st < NS; ++st)
-        #pragma unroll
-        for (int m = 0; m < NMAT; ++m)
-            #pragma unroll
-            for (int tt = 0; tt < 8; ++tt) acc[st][m][tt] = (f32x4) {0.f, 0.f, 0.f, 0.f};
-    stage(0, xs0);
-    static_for<D>([&](auto sc) {
-        fetch(decltype(sc)::value, sc);
-        __builtin_amdgcn_sched_barrier(0);                  // keep the ring's issue order (waits count in order)
-    });
-    for (int kg0 = 0; kg0 < KG; kg0 += D)
-    {
-        static_for<D>([&](auto sc) {
+        };
+        PFetch<DENSE, NMAT, NS> ring[D];
+        auto fetch = [&](int kg, auto sc) {
             constexpr int s = decltype(sc)::value;
-            const int kg = kg0 + s;
-            const bool even = (kg & 1) == 0;
-            u32x4* cur = even ? xs0 : xs1;
-            // this wave's staged loads of group kg are older than the FETCH_LOADS of the last refill (or, for kg = 0,
-            // than the D prologue refills); the barrier then makes every wave's group kg visible
-            if (kg == 0) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(FETCH_LOADS * D) : "memory");
-            else asm volatile("s_waitcnt vmcnt(%0)" :: "n"(FETCH_LOADS) : "memory");
-            __syncthreads();
-            if (kg + 1 < KG) stage(kg + 1, even ? xs1 : xs0);
-            f16x2 sh[NS][NMAT];
             #pragma unroll
             for (int st = 0; st < NS; ++st)
                 #pragma unroll
                 for (int m = 0; m < NMAT; ++m)
                 {
-                    const _Float16 h = DENSE ? (_Float16) 1.0f : (_Float16) bf2f(ring[s].s[st][m]);
-                    sh[st][m] = (f16x2) {h, h};
+                    const int nb = nb0 + st;
+                    if (DENSE)
+                    {
+                        #pragma unroll
+                        for (int u = 0; u < 4; ++u) ring[s].q[st][m][u] = ldw16(wp[m] + ((size_t) (nb * KS + kg * 4 + u) * 64 + l) * 16);
+                    }
+                    else
+                    {
+                        ring[s].q[st][m][0] = ldw16(wp[m] + ((size_t) (nb * KG + kg) * 64 + l) * 16);
+                        ring[s].s[st][m] = ldg<uint16_t>(sp[m] + ((size_t) (nb * 16 + row) * KG + kg) * 2);
+                    }
                 }
+        };
+        f32x4 acc[NS][NMAT][8];
+        #pragma unroll
+        for (int st = 0; st < NS; ++st)
             #pragma unroll
-            for (int k = 0; k < 4; ++k)
-            {
-                f16x8 a[NS][NMAT];
+            for (int m = 0; m < NMAT; ++m)
+                #pragma unroll
+                for (int tt = 0; tt < 8; ++tt) acc[st][m][tt] = (f32x4) {0.f, 0.f, 0.f, 0.f};
+        stage(0, xs0);
+        static_for<D>([&](auto sc) {
+            fetch(decltype(sc)::value, sc);
+            __builtin_amdgcn_sched_barrier(0);                  // keep the ring's issue order (waits count in order)
+        });
+        for (int kg0 = 0; kg0 < KG; kg0 += D)
+        {
+            static_for<D>([&](auto sc) {
+                constexpr int s = decltype(sc)::value;
+                const int kg = kg0 + s;
+                const bool even = (kg & 1) == 0;
+                u32x4* cur = even ? xs0 : xs1;
+                // this wave's staged loads of group kg are older than the FETCH_LOADS of the last refill (or, for kg = 0,
+                // than the D prologue refills); the barrier then makes every wave's group kg visible
+                if (kg == 0) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(FETCH_LOADS * D) : "memory");
+                else asm volatile("s_waitcnt vmcnt(%0)" :: "n"(FETCH_LOADS) : "memory");
+                __syncthreads();
+                if (kg + 1 < KG) stage(kg + 1, even ? xs1 : xs0);
+                f16x2 sh[NS][NMAT];
                 #pragma unroll
                 for (int st = 0; st < NS; ++st)
                     #pragma unroll
                     for (int m = 0; m < NMAT; ++m)
-                        a[st][m] = DENSE ? as_f16x8(ring[s].q[st][m][k]) : dq8s(ring[s].q[st][m][0][k], sh[st][m], dq);
-                // the k step's input tiles read together (tiles past the block read stale LDS data, never used), so
-                // the LDS latency is paid once per k step rather than once per tile
-                f16x8 bvs[8];
+                    {
+                        const _Float16 h = DENSE ? (_Float16) 1.0f : (_Float16) bf2f(ring[s].s[st][m]);
+                        sh[st][m] = (f16x2) {h, h};
+                    }
                 #pragma unroll
-                for (int tt = 0; tt < 8; ++tt) bvs[tt] = as_f16x8(cur[(tt * 4 + k) * 64 + l]);
-                #pragma unroll
-                for (int tt = 0; tt < 8; ++tt)
+                for (int k = 0; k < 4; ++k)
                 {
-                    if (tt >= ntt) break;
+                    f16x8 a[NS][NMAT];
                     #pragma unroll
                     for (int st = 0; st < NS; ++st)
                         #pragma unroll
-                        for (int m = 0; m < NMAT; ++m) acc[st][m][tt] = mfma16(a[st][m], bvs[tt], acc[st][m][tt]);
+                        for (int m = 0; m < NMAT; ++m)
+                            a[st][m] = DENSE ? as_f16x8(ring[s].q[st][m][k]) : dq8s(ring[s].q[st][m][0][k], sh[st][m], dq);
+                    // the k step's input tiles read together (tiles past the block read stale LDS data, never used), so
+                    // the LDS latency is paid once per k step rather than once per tile
+                    f16x8 bvs[8];
+                    #pragma unroll
+                    for (int tt = 0; tt < 8; ++tt) bvs[tt] = as_f16x8(cur[(tt * 4 + k) * 64 + l]);
+                    #pragma unroll
+                    for (int tt = 0; tt < 8; ++tt)
+                    {
+                        if (tt >= ntt) break;
+                        #pragma unroll
+                        for (int st = 0; st < NS; ++st)
+                            #pragma unroll
+                            for (int m = 0; m < NMAT; ++m) acc[st][m][tt] = mfma16(a[st][m], bvs[tt], acc[st][m][tt]);
+                    }
                 }
-            }
-            fetch(min(kg + D, KG - 1), sc);                 // refill the slot just used (clamped at the end)
-        });
-    }
-    // epilogue: lane holds output rows 4(l/16)..+4 of pick tt*16 + l%16
-    #pragma unroll
-    for (int tt = 0; tt < 8; ++tt)
-    {
-        const int pk = tt * 16 + row;
-        if (pk >= b.rows) continue;
+                fetch(min(kg + D, KG - 1), sc);                 // refill the slot just used (clamped at the end)
+            });
+        }
+        // epilogue: lane holds output rows 4(l/16)..+4 of pick tt*16 + l%16
         #pragma unroll
-        for (int st = 0; st < NS; ++st)
+        for (int tt = 0; tt < 8; ++tt)
         {
-            const int n = (nb0 + st) * 16 + 4 * (l >> 4);
-            if (NMAT == 2)
+            const int pk = tt * 16 + row;
+            if (pk >= b.rows) continue;
+            #pragma unroll
+            for (int st = 0; st < NS; ++st)
             {
-                const float wv = DENSE ? 1.0f : wt[b.p0 + pk];
-                _Float16 o[4];
-                #pragma unroll
-                for (int i = 0; i < 4; ++i) o[i] = (_Float16) (silu(acc[st][0][tt][i]) * acc[st][NMAT - 1][tt][i] * wv);
-                *(uint2*) (ar + (size_t) (off + b.p0 + pk) * NOUT + n) = *(const uint2*) o;
+                const int n = (nb0 + st) * 16 + 4 * (l >> 4);
+                if (EPI == EPI_RAW)
+                {
+                    #pragma unroll
+                    for (int m = 0; m < NMAT; ++m)
+                        *(f32x4*) (dout + ((size_t) m * ps + b.p0 + pk) * NOUT + n) = acc[st][m][tt];
+                }
+                else if (EPI == EPI_ACT)
+                {
+                    const float wv = DENSE ? 1.0f : wt[b.p0 + pk];
+                    _Float16 o[4];
+                    #pragma unroll
+                    for (int i = 0; i < 4; ++i) o[i] = (_Float16) (silu(acc[st][0][tt][i]) * acc[st][NMAT - 1][tt][i] * wv);
+                    *(uint2*) (ar + (size_t) (off + b.p0 + pk) * NOUT + n) = *(const uint2*) o;
+                }
+                else if (EPI == EPI_FIN)
+                {
+                    // out[tok] += acc (the combine in the epilogue, fp32 atomics as moe4t.cu's down GEMM: no d buffer)
+                    const int tk = tok[b.p0 + pk];
+                    if ((unsigned) tk < (unsigned) T)
+                    {
+                        float* o = fout + (size_t) tk * NOUT + n;
+                        #pragma unroll
+                        for (int i = 0; i < 4; ++i) unsafeAtomicAdd(o + i, acc[st][0][tt][i]);
+                    }
+                }
+                else *(f32x4*) (dout + (size_t) (off + b.p0 + pk) * NOUT + n) = acc[st][0][tt];
             }
-            else *(f32x4*) (dout + (size_t) (off + b.p0 + pk) * NOUT + n) = acc[st][0][tt];
         }
     }
 }
@@ -353,18 +386,6 @@ __global__ void __launch_bounds__(256) pfin_kernel(const float* __restrict__ d, 
     }
 }
 
-// fin with atomics (p4_fin_kernel, moe4p.cu:195-206)
-__global__ void __launch_bounds__(256) pfin_atomic_kernel(const float* __restrict__ d, const int* __restrict__ tok,
-                                                          int npos, const int* __restrict__ meta, int T,
-                                                          float* __restrict__ out)
-{
-    const int p = blockIdx.x;
-    if (p >= npos || (meta && p >= meta[0])) return;
-    const int tk = tok[p];
-    if ((unsigned) tk >= (unsigned) T) return;
-    for (int n = threadIdx.x; n < H; n += 256) atomicAdd(out + (size_t) tk * H + n, d[(size_t) p * H + n]);
-}
-
 }  // namespace hmoe
 
 using namespace hmoe;
@@ -386,7 +407,8 @@ extern "C" int hmoe_dispatch(const int64_t* sel, const uint16_t* rw, int T, int 
                              int* meta, void* work, void* stream)
 {
     HMOE_REQUIRE(sel && rw && counts && tok && eid && wt && inv && rbt && meta && work, "dispatch: null buffer");
-    HMOE_REQUIRE(T >= 1 && topk >= 1 && topk <= TOPK && n >= 1 && n <= 256 && lo >= 0 && bm >= 1 && nrb_max >= 1,
+    HMOE_REQUIRE(T >= 1 && topk >= 1 && topk <= TOPK && n >= 1 && n <= 256 && lo >= 0 && bm >= 1 && bm <= 2 * PB &&
+                 nrb_max >= 1,
                  "dispatch: T %d topk %d n %d bm %d", T, topk, n, bm);
     const int F = T * topk, nblk = (F + DBLK - 1) / DBLK;
     int* hist = (int*) work;
@@ -449,23 +471,31 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
                  "moe4p_forward: the shared expert needs the inverse map and the gu scratch (256-byte aligned)");
     HMOE_REQUIRE(((uintptr_t) x & 15) == 0 && ((uintptr_t) ar & 15) == 0 && ((uintptr_t) d & 15) == 0 &&
                  ((uintptr_t) out & 15) == 0, "moe4p_forward: alignment");
+    HMOE_REQUIRE(xf == HMOE_XF_BF16 || xf == HMOE_XF_F16, "moe4p_forward: xf must be HMOE_XF_BF16 (0) or HMOE_XF_F16 "
+                 "(2); the reference's fragment-order x (xf = 1) is not supported");
     hipStream_t st = (hipStream_t) stream;
     const uint16_t* xb = (const uint16_t*) x;
-    if (!xf)
+    if (xf == HMOE_XF_BF16)
     {
         HMOE_REQUIRE(gu && ((uintptr_t) gu & 15) == 0, "moe4p_forward: xf = 0 needs the gu scratch (the f16 copy of x)");
         to_f16_kernel<<<1024, 256, 0, st>>>(xb, (size_t) T * H, (_Float16*) gu);
         xb = (const uint16_t*) gu;
     }
     _Float16* a = (_Float16*) ar;
-    // gate/up: 64 x 2 output columns per workgroup (NS 2); down: 64 x 4 (NS 4)
+    // gate/up: 64 x 2 output columns per workgroup (NS 2); down: 64 x 4 (NS 4), into d rows for the ordered combine
+    // (inv given) or added into out[tok] by its epilogue (no inverse map: the atomic combine of p4_fin_kernel)
     if (nrb > 0)
     {
         pgemm_kernel<false, 2, 2, 3><<<dim3(nrb, I / 128), PT, 0, st>>>((const _Float16*) xb, tok, wt, rbt, nrb, meta, n_tab, gw, uw,
                                                                              gs, us, nullptr, nullptr, a, nullptr, T, 0);
-        pgemm_kernel<false, 1, 4, 2><<<dim3(nrb, H / 256), PT, 0, st>>>(a, nullptr, nullptr, rbt,
-                                                                               nrb, meta, n_tab, dw, nullptr, ds, nullptr,
-                                                                               nullptr, nullptr, nullptr, d, T, 0);
+        if (inv)
+            pgemm_kernel<false, 1, 4, 2><<<dim3(nrb, H / 256), PT, 0, st>>>(a, nullptr, nullptr, rbt,
+                                                                                   nrb, meta, n_tab, dw, nullptr, ds, nullptr,
+                                                                                   nullptr, nullptr, nullptr, d, T, 0);
+        else
+            pgemm_kernel<false, 1, 4, 2, EPI_FIN><<<dim3(nrb, H / 256), PT, 0, st>>>(a, tok, nullptr, rbt, nrb, meta, n_tab,
+                                                                                    dw, nullptr, ds, nullptr, nullptr,
+                                                                                    nullptr, nullptr, nullptr, T, 0, out);
     }
     const bool sh = sh_gw != nullptr;
     if (sh)
@@ -491,6 +521,139 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
             return rc;
     }
     if (inv) pfin_kernel<<<T, 256, 0, st>>>(d, inv, topk, sh ? ps : -1, out);
-    else if (npos > 0) pfin_atomic_kernel<<<npos, 256, 0, st>>>(d, tok, npos, meta, T, out);
     return HMOE_LAUNCHED("moe4p_forward");
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// the shared expert alone over a chunk (the reference runs it through the model's own shared-expert MLP at prefill,
+// runtime/tier/tier_split.py:548-560): out += down(silu(gate x) * up x)
+// ---------------------------------------------------------------------------------------------------------------
+namespace hmoe {
+
+// out[t] += d[t] (each element has one writer: deterministic)
+__global__ void __launch_bounds__(256) add_rows_kernel(const float* __restrict__ d, size_t n, float* __restrict__ out)
+{
+    for (size_t i = (blockIdx.x * (size_t) 256 + threadIdx.x) * 4; i < n; i += (size_t) gridDim.x * 256 * 4)
+        *(f32x4*) (out + i) = *(const f32x4*) (out + i) + *(const f32x4*) (d + i);
+}
+
+// work layout: x f16 copy [T][H] | g|u fp32 [T][2I] | act f16 [T][I] | d fp32 [T][H] | library workspace
+static size_t shw_x(int T) { return 0; }
+static size_t shw_gu(int T) { return ((size_t) T * H * 2 + 255) & ~(size_t) 255; }
+static size_t shw_act(int T) { return shw_gu(T) + (size_t) T * 2 * I * 4; }
+static size_t shw_d(int T) { return shw_act(T) + (((size_t) T * I * 2 + 255) & ~(size_t) 255); }
+static size_t shw_ws(int T) { return shw_d(T) + (size_t) T * H * 4; }
+
+}  // namespace hmoe
+
+extern "C" size_t hmoe_shared_work_bytes(int T) { return shw_ws(T > 0 ? T : 1) + SH_WS; }
+
+extern "C" int hmoe_shared_forward(const void* x, int T, const void* sh_gw, const void* sh_uw, const void* sh_dw,
+                                   void* work, float* out, int xf, void* stream)
+{
+    if (T == 0) return HMOE_OK;
+    HMOE_REQUIRE(x && sh_gw && sh_uw && sh_dw && work && out && T > 0, "shared_forward: arguments");
+    HMOE_REQUIRE(xf == HMOE_XF_BF16 || xf == HMOE_XF_F16, "shared_forward: xf must be HMOE_XF_BF16 (0) or HMOE_XF_F16 (2)");
+    HMOE_REQUIRE(((uintptr_t) x & 15) == 0 && ((uintptr_t) work & 255) == 0 && ((uintptr_t) out & 15) == 0,
+                 "shared_forward: alignment (x, out 16 bytes, work 256)");
+    hipStream_t st = (hipStream_t) stream;
+    uint8_t* wk = (uint8_t*) work;
+    const _Float16* xs = (const _Float16*) x;
+    if (xf == HMOE_XF_BF16)
+    {
+        to_f16_kernel<<<1024, 256, 0, st>>>((const uint16_t*) x, (size_t) T * H, (_Float16*) (wk + shw_x(T)));
+        xs = (const _Float16*) (wk + shw_x(T));
+    }
+    float* c = (float*) (wk + shw_gu(T));
+    _Float16* a = (_Float16*) (wk + shw_act(T));
+    float* d = (float*) (wk + shw_d(T));
+    void* ws = wk + shw_ws(T);
+    if ((const _Float16*) sh_uw == (const _Float16*) sh_gw + (size_t) I * H)
+    {
+        if (int rc = lt_gemm((const _Float16*) sh_gw, xs, c, 2 * I, T, H, 2 * I, ws, SH_WS, st)) return rc;
+    }
+    else
+    {
+        if (int rc = lt_gemm((const _Float16*) sh_gw, xs, c, I, T, H, 2 * I, ws, SH_WS, st)) return rc;
+        if (int rc = lt_gemm((const _Float16*) sh_uw, xs, c + I, I, T, H, 2 * I, ws, SH_WS, st)) return rc;
+    }
+    sh_swiglu_kernel<<<(unsigned) (((size_t) T * I / 4 + 255) / 256), 256, 0, st>>>(c, T, a);
+    if (int rc = lt_gemm((const _Float16*) sh_dw, a, d, H, T, I, H, ws, SH_WS, st)) return rc;
+    add_rows_kernel<<<1024, 256, 0, st>>>(d, (size_t) T * H, out);
+    return HMOE_LAUNCHED("shared_forward");
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// long prefill: runtime/tier/moe4/moe4t.cu:476-524 (moe4t.gemm / scratch / forward)
+// ---------------------------------------------------------------------------------------------------------------
+extern "C" size_t hmoe_moe4t_scratch_bytes(int which, int npos)
+{
+    const size_t n = npos > 0 ? (size_t) npos : 1;
+    switch (which)
+    {
+        case 0: return 2 * n * I * 4;                                   // gu fp32 [2][npos][I] (unused)
+        case 1: return n * I * 2;                                       // ar f16 [npos][I]
+        case 2: return n * H * 4;                                       // d fp32 [1][npos][H]: the f16 copy of bf16 x
+        default: return 0;
+    }
+}
+
+extern "C" int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid, const float* wt, const int* rbt,
+                                  int npos, int nrb, int n_tab, const int64_t* gw, const int64_t* uw, const int64_t* dw,
+                                  const int64_t* gs, const int64_t* us, const int64_t* ds, float* gu, uint16_t* ar,
+                                  float* d, float* out, int ps, const int* meta, int T, int xf, void* stream)
+{
+    (void) eid; (void) gu;
+    if (npos == 0) return HMOE_OK;                                      // moe4t.cu:508: no pick, no work
+    HMOE_REQUIRE(x && tok && wt && rbt && ar && out, "moe4t_forward: null buffer");
+    HMOE_REQUIRE(npos > 0 && nrb >= 0 && npos <= ps && T >= 1, "moe4t_forward: npos %d nrb %d ps %d T %d", npos, nrb, ps,
+                 T);
+    HMOE_REQUIRE(n_tab >= 1 && n_tab <= HMOE_MAXE && gw && uw && dw && gs && us && ds, "moe4t_forward: tables");
+    HMOE_REQUIRE(xf == HMOE_XF_BF16 || xf == HMOE_XF_F16, "moe4t_forward: xf must be HMOE_XF_BF16 (0) or HMOE_XF_F16 (2)");
+    HMOE_REQUIRE(((uintptr_t) x & 15) == 0 && ((uintptr_t) ar & 15) == 0 && ((uintptr_t) out & 15) == 0 &&
+                 ((uintptr_t) d & 15) == 0, "moe4t_forward: alignment");
+    hipStream_t st = (hipStream_t) stream;
+    const _Float16* xh = (const _Float16*) x;
+    if (xf == HMOE_XF_BF16)
+    {
+        // the f16 copy of x in d (the reference gathers the picks' rows into d; T rows fit: T * H * 2 <= npos * H * 4
+        // whenever every token has a pick, and the check below holds it in general)
+        HMOE_REQUIRE(d && (size_t) T * H * 2 <= (size_t) ps * H * 4, "moe4t_forward: bf16 x needs d for its f16 copy");
+        to_f16_kernel<<<1024, 256, 0, st>>>((const uint16_t*) x, (size_t) T * H, (_Float16*) d);
+        xh = (const _Float16*) d;
+    }
+    if (nrb > 0)
+    {
+        pgemm_kernel<false, 2, 2, 3><<<dim3(nrb, I / 128), PT, 0, st>>>(xh, tok, wt, rbt, nrb, meta, n_tab, gw, uw, gs,
+                                                                             us, nullptr, nullptr, (_Float16*) ar,
+                                                                             nullptr, T, 0);
+        pgemm_kernel<false, 1, 4, 2, EPI_FIN><<<dim3(nrb, H / 256), PT, 0, st>>>((const _Float16*) ar, tok, nullptr,
+                                                                                rbt, nrb, meta, n_tab, dw, nullptr, ds,
+                                                                                nullptr, nullptr, nullptr, nullptr,
+                                                                                nullptr, T, 0, out);
+    }
+    return HMOE_LAUNCHED("moe4t_forward");
+}
+
+extern "C" int hmoe_moe4t_gemm(const void* xs, int rows, const int* rbt, int nrb, int n_tab, const int64_t* w0,
+                               const int64_t* w1, const int64_t* s0, const int64_t* s1, float* out, int ps, int down,
+                               void* stream)
+{
+    HMOE_REQUIRE(xs && rbt && out && w0 && s0 && (down || (w1 && s1)), "moe4t_gemm: null buffer");
+    HMOE_REQUIRE(rows >= 1 && nrb >= 0 && ps >= rows && n_tab >= 1 && n_tab <= HMOE_MAXE,
+                 "moe4t_gemm: rows %d nrb %d ps %d n_tab %d", rows, nrb, ps, n_tab);
+    HMOE_REQUIRE(((uintptr_t) xs & 15) == 0 && ((uintptr_t) out & 15) == 0, "moe4t_gemm: alignment");
+    if (nrb == 0) return HMOE_OK;
+    hipStream_t st = (hipStream_t) stream;
+    if (down)
+        pgemm_kernel<false, 1, 4, 2><<<dim3(nrb, H / 256), PT, 0, st>>>((const _Float16*) xs, nullptr, nullptr, rbt,
+                                                                               nrb, nullptr, n_tab, w0, nullptr, s0,
+                                                                               nullptr, nullptr, nullptr, nullptr, out,
+                                                                               rows, 0);
+    else
+        pgemm_kernel<false, 2, 2, 3, EPI_RAW><<<dim3(nrb, I / 128), PT, 0, st>>>((const _Float16*) xs, nullptr, nullptr,
+                                                                                rbt, nrb, nullptr, n_tab, w0, w1, s0,
+                                                                                s1, nullptr, nullptr, nullptr, out,
+                                                                                rows, 0, nullptr, ps);
+    return HMOE_LAUNCHED("moe4t_gemm");
 }

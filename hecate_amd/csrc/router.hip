@@ -155,7 +155,9 @@ using namespace hmoe;
 extern "C" size_t hmoe_router_scratch_bytes(int R, int E)
 {
     (void) E;
-    return (size_t) RSEG * (size_t) (R > 0 ? R : 1) * RMAXE * sizeof(float);
+    // R <= MAXR: one logits row per row (the small path); more rows: the segment planes of the large path
+    const size_t r = R > 0 ? (size_t) R : 1;
+    return (R <= MAXR ? 1 : RSEG) * r * RMAXE * sizeof(float);
 }
 
 extern "C" int hmoe_router_fused(const void* x, const float* wt, const float* bias, float* logits, int* ctr,

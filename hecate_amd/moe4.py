@@ -1,12 +1,13 @@
 """Decode MoE operator: the drop-in for the reference's `moe4` extension (runtime/tier/moe4/moe4.cu:897-925).
 
 Same op names and argument order as the reference's pybind module; formats are this build's gfx950 ones
-(include/hecate_moe.h): x bf16 (or its f16 copy with xf=1), I4G128 experts with bf16 group-128 scales, the shared
+(include/hecate_moe.h): x row-major bf16 or fp16 (the reference's fp16 x with xf=0 works unchanged; its fragment-order
+xf=1 is refused), I4G128 experts with bf16 group-128 scales, the shared
 expert as F16T. Work runs on the current torch stream; errors raise RuntimeError like TORCH_CHECK.
 """
 import torch
 
-from ._lib import call, lib, on_device, ptr, stream_of
+from ._lib import call, lib, on_device, ptr, stream_of, xf_of
 
 H, I, TOPK, MAXR = 6144, 2048, 8, 16
 
@@ -40,7 +41,8 @@ def forward(x, sel, rw, n_hot, gate_w, up_w, down_w, gate_s, up_s, down_s, act, 
     R = x.shape[0]
     on_device("moe4", x, sel, rw, gate_w, up_w, down_w, gate_s, up_s, down_s, act, gu32, ctr_a, y32, ctr_b, y)
     _req(1 <= R <= MAXR and x.shape[-1] == H, f"x shape {tuple(x.shape)}")
-    _req(x.dtype == (torch.float16 if xf else torch.bfloat16) and x.is_contiguous() and x.is_cuda, "x dtype / layout")
+    fmt = xf_of(x, xf)
+    _req(x.is_contiguous() and x.is_cuda, "x layout")
     _req(sel.dtype == torch.int64 and sel.is_contiguous() and sel.shape == (R, TOPK),
          "selection must be contiguous int64 [R, 8]")
     _req(rw.dtype == torch.float16 and rw.is_contiguous() and rw.shape == (R, TOPK), "routing weights f16 [R, 8]")
@@ -50,14 +52,14 @@ def forward(x, sel, rw, n_hot, gate_w, up_w, down_w, gate_s, up_s, down_s, act, 
     call("hmoe_moe4_forward", ptr(x), ptr(sel), ptr(rw), R, int(n_hot), ptr(gate_w), ptr(up_w), ptr(down_w),
          ptr(gate_s), ptr(up_s), ptr(down_s), ptr(act), ptr(gu32), ptr(ctr_a), ptr(y32), ptr(ctr_b), ptr(y),
          int(blocks), int(blocks_a), int(lo), _addr(sh_gw), _addr(sh_uw), _addr(sh_dw), _addr(sh_gs), _addr(sh_us),
-         _addr(sh_ds), int(xf), stream_of(x.device))
+         _addr(sh_ds), fmt, stream_of(x.device))
 
 
 def gate_up(x, sel, rw, n_hot, gate_w, up_w, gate_s, up_s, act, gu32, ctr_a, blocks, lo, sh_gw=0, sh_uw=0, xf=0):
     """phase 1 of forward: act of the routed experts (and the shared expert)"""
     on_device("moe4.gate_up", x, sel, rw, gate_w, up_w, gate_s, up_s, act, gu32, ctr_a)
     call("hmoe_moe4_gate_up", ptr(x), ptr(sel), ptr(rw), x.shape[0], int(n_hot), ptr(gate_w), ptr(up_w), ptr(gate_s),
-         ptr(up_s), ptr(act), ptr(gu32), ptr(ctr_a), int(blocks), int(lo), _addr(sh_gw), _addr(sh_uw), int(xf),
+         ptr(up_s), ptr(act), ptr(gu32), ptr(ctr_a), int(blocks), int(lo), _addr(sh_gw), _addr(sh_uw), xf_of(x, xf),
          stream_of(x.device))
 
 

@@ -6,7 +6,7 @@ from a device-side dispatch plan (no host sync), and the shared expert in the sa
 """
 import torch
 
-from ._lib import call, lib, on_device, ptr, stream_of
+from ._lib import XF_BF16, call, lib, on_device, ptr, stream_of, xf_of
 
 H, I = 6144, 2048
 
@@ -31,7 +31,7 @@ def forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, inv=No
     if shared is not None and not all(w.dtype == torch.float16 and w.is_contiguous() and w.numel() == I * H
                                       for w in shared):
         raise RuntimeError("moe4p: the shared expert is row-major f16 gate [I, H], up [I, H], down [H, I]")
-    xf = 1 if x.dtype == torch.float16 else 0
+    xf = xf_of(x)
     if not (x.dim() == 2 and x.shape[1] == H and x.dtype in (torch.bfloat16, torch.float16) and out.dtype == torch.float32
             and rbt.dim() == 2 and rbt.shape[1] == 4 and x.is_contiguous() and out.is_contiguous()):
         raise RuntimeError("moe4p: shapes")
@@ -42,7 +42,7 @@ def forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, inv=No
         raise RuntimeError(f"moe4p: scratch holds {ps} picks, {npos} given")
     # the scratch at least as large as the library writes it (a short one would be written past its end): gu holds
     # the f16 copy of x when x is bf16, and the shared expert's sums and GEMM workspace when it is given
-    need = int(lib().hmoe_moe4p_scratch_bytes(0, ps, T)) if shared is not None else (T * H * 2 if xf == 0 else 0)
+    need = int(lib().hmoe_moe4p_scratch_bytes(0, ps, T)) if shared is not None else (T * H * 2 if xf == XF_BF16 else 0)
     if need and (gu is None or gu.numel() * gu.element_size() < need):
         raise RuntimeError(f"moe4p: the gu scratch needs {need} bytes")
     if ar.dim() != 2 or ar.shape[1] != I or d.dim() != 2 or d.shape[1] != H:

@@ -1,7 +1,7 @@
 """Fused sigmoid + bias top-k router: the drop-in for runtime/core/exl3_router.py:134-146 router_fused.
 
 router_fused(x, wt, bias, logits, ctr, sel, rw, topk, scale) keeps the reference's arguments (x bf16 here, wt fp32
-[E, K]); the trailing xh receives an f16 copy of x for moe4.forward(xf=1). Any row count (the reference handles 2..8).
+[E, K]); the trailing xh receives an f16 copy of x (moe4.forward reads fp16 x as the reference does). Any row count (the reference handles 2..8).
 """
 import torch
 

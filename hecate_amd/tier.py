@@ -2,7 +2,7 @@
 (tier_split_load:171-269 resident expert tables, tier_submit:520-574 decode vs prefill, tier_combine:577-644) and the
 row-block planner of runtime/tier/rtx_split.py:236-255 (pick_groups), restated for this build's formats.
 
-Decode (<= 16 rows): router_fused (writes the f16 copy of x) -> moe4.forward(xf=1) (routed + shared expert into the
+Decode (<= 16 rows): router_fused (writes the f16 copy of x) -> moe4.forward (routed + shared expert into the
 fp32 accumulator) -> bf16 output (accumulator zeroed). Prefill: router -> device dispatch plan (no host sync) ->
 moe4p.forward (routed + shared) -> bf16 output. Every launch is static-shaped and allocation-free, so a whole step can
 be captured in a hipGraph.
@@ -10,10 +10,11 @@ be captured in a hipGraph.
 import numpy as np
 import torch
 
-from . import moe4, moe4p, router
+from . import moe4, moe4p, moe4t, router
 from ._lib import call, lib, on_device, ptr, stream_of
 
 H, I, TOPK = 6144, 2048, 8
+LONG_ROWS = 2048        # EXL3_PREFILL_GB300_ROWS: longer chunks run on moe4t with 256-pick blocks (tier_split.py:543)
 I4_Q_GU, I4_S_GU = I * H // 2, I * (H // 128) * 2          # bytes of one gate / up matrix (codes, scales)
 I4_Q_D, I4_S_D = H * I // 2, H * (I // 128) * 2            # bytes of one down matrix
 
@@ -121,10 +122,10 @@ def f16t_rows(t, N, K):
 class PrefillBuffers:
     """device buffers of a prefill chunk of up to T rows: selection, dispatch plan (hmoe_dispatch), GEMM scratch"""
 
-    def __init__(self, T, topk, lo, n, E, device, bm=128):
+    def __init__(self, T, topk, lo, n, E, device, bm=128, long=False):
         dev = torch.device(device)
         L = lib()
-        self.T, self.topk, self.lo, self.n, self.bm = T, topk, lo, n, bm
+        self.T, self.topk, self.lo, self.n, self.bm, self.long = T, topk, lo, n, bm, long
         self.F = F = T * topk
         self.nrb_max = int(L.hmoe_dispatch_nrb_max(F, n, bm))
         z = lambda *shape, dt=torch.int32: torch.zeros(shape, dtype=dt, device=dev)
@@ -132,7 +133,13 @@ class PrefillBuffers:
         self.wt = z(F, dt=torch.float32)
         self.rbt, self.meta = z(self.nrb_max, 4), z(4)
         self.work = z(int(L.hmoe_dispatch_work_bytes(T, topk, n)) // 4 + 1)
-        self.scr = moe4p.scratch(dev, F, T)
+        if long:
+            # moe4t's ar and d (its gu is unused: not allocated) and the shared expert's work
+            self.scr = [None, torch.empty((F, I), dtype=torch.float16, device=dev),
+                        torch.empty((1, F, H), dtype=torch.float32, device=dev)]
+            self.shw = torch.empty(int(L.hmoe_shared_work_bytes(T)) // 4 + 64, dtype=torch.float32, device=dev)
+        else:
+            self.scr = moe4p.scratch(dev, F, T)
         self.y = z(T, H, dt=torch.float32)
         self.out = z(T, H, dt=torch.bfloat16)
         self.xh = z(T, H, dt=torch.float16)                        # the router's f16 copy of x (the GEMM input)
@@ -190,12 +197,12 @@ class MoELayer:
         xh = self.xh if xh is None else xh
         if events is None:
             moe4.forward(xh[:R], self.sel[:R], self.rw[:R], self.n_hot, gq, uq, dq, gs, us, ds, *self.scr, y, blocks,
-                         0, self.lo, sh[0], sh[1], sh[2], 0, 0, 0, xf=1)
+                         0, self.lo, sh[0], sh[1], sh[2], 0, 0, 0)
             return
         act, gu32, ctr_a, y32, ctr_b = self.scr
         events[0].record()
         moe4.gate_up(xh[:R], self.sel[:R], self.rw[:R], self.n_hot, gq, uq, gs, us, act, gu32, ctr_a, blocks, self.lo,
-                     sh[0], sh[1], xf=1)
+                     sh[0], sh[1])
         events[1].record()
         moe4.down(self.sel[:R], self.rw[:R], self.n_hot, dq, ds, act, y32, ctr_b, y, blocks, self.lo, sh[2])
         events[2].record()
@@ -221,9 +228,12 @@ class MoELayer:
 
     # ---- prefill ----------------------------------------------------------------------------------------------
     def _prefill_buffers(self, T):
-        if self._pf is not None and self._pf.T >= T:
+        long = T > LONG_ROWS
+        if self._pf is not None and self._pf.T >= T and self._pf.long == long:
             return self._pf
-        self._pf = PrefillBuffers(T, self.topk, self.lo, self.n_hot, self.E, self.device)
+        self._pf = None
+        self._pf = PrefillBuffers(T, self.topk, self.lo, self.n_hot, self.E, self.device, bm=256 if long else 128,
+                                  long=long)
         return self._pf
 
     def prefill_experts(self, x, y, with_shared=True):
@@ -231,6 +241,14 @@ class MoELayer:
         T = x.shape[0]
         pf = self._pf
         gq, uq, dq, gs, us, ds = self.bank.tables()
+        if pf.long:
+            # tier_split.py:427-462: every routed expert on moe4t (256-pick balanced blocks, the down GEMM adding into
+            # y), the shared expert apart
+            moe4t.forward(x, pf.tok, pf.eid, pf.wt, pf.rbt, gq, uq, dq, gs, us, ds, *pf.scr, y, meta=pf.meta,
+                          npos=pf.F, nrb=pf.nrb_max)
+            if with_shared and self.shared is not None:
+                moe4t.shared(x, *self.shared_rows(), pf.shw, y)
+            return
         sh = self.shared_rows() if (with_shared and self.shared is not None) else None
         moe4p.forward(x, pf.tok, pf.eid, pf.wt, pf.rbt, gq, uq, dq, gs, us, ds, *pf.scr, y,
                       inv=pf.inv[:T * self.topk], meta=pf.meta, topk=self.topk, shared=sh, npos=pf.F, nrb=pf.nrb_max)
@@ -247,7 +265,8 @@ class MoELayer:
 
     def prefill(self, x, with_shared=True):
         """the prefill layer: bf16 [T, H] out (router, device dispatch plan, grouped GEMMs, per-token combine); an
-        empty chunk gives an empty output (tier_split.py:377 returns out when no pick reaches the tier)"""
+        empty chunk gives an empty output (tier_split.py:377 returns out when no pick reaches the tier). Chunks of more
+        than LONG_ROWS rows run the routed experts on moe4t (256-pick blocks, atomic combine), as the reference does"""
         T = x.shape[0]
         on_device("prefill", x, self.wg)
         if T == 0:
@@ -255,7 +274,7 @@ class MoELayer:
         pf = self._prefill_buffers(T)
         sel, rw = pf.sel[:T], pf.rw[:T]
         router.router_fused(x, self.wg, self.bias, pf.logits, self.ctr, sel, rw, self.topk, self.scale, pf.xh[:T])
-        pf.run(sel, rw)
+        pf.run(sel, rw, balance=True)
         y = pf.y[:T]
         self.prefill_experts(pf.xh[:T], y, with_shared)
         return moe4.finish_bf16(y, T, pf.out[:T])

@@ -40,6 +40,13 @@ extern "C" {
 
 enum { HMOE_OK = 0, HMOE_ERR_ARG = 1, HMOE_ERR_HIP = 2 };
 
+/* the x format flag `xf` of the decode and prefill ops. The reference's moe4.forward takes fp16 row-major x with xf = 0
+ * and x in mma B-fragment order (as its fused norm kernel writes it) with xf = 1 (runtime/tier/moe4/moe4.cu:826); a C
+ * ABI cannot see a dtype, so this build names each format: bf16 row-major (BASELINE's activation type), the
+ * reference's fragment order (refused with HMOE_ERR_ARG: an NVIDIA mma layout, never produced on gfx950), and fp16
+ * row-major (the reference's xf = 0 data; the Python mirror maps an fp16 tensor with xf = 0 to it) */
+enum { HMOE_XF_BF16 = 0, HMOE_XF_FRAG = 1, HMOE_XF_F16 = 2 };
+
 /* last error message of the calling thread ("" if none) */
 const char* hmoe_last_error(void);
 /* ABI version of this library */
@@ -67,16 +74,19 @@ int hmoe_gen_normal(uint64_t key, int64_t n, float mean, float sigma, int dtype,
 /* ---- router: runtime/core/exl3_router.py:134-146 router_fused(x, wt, bias, logits, ctr, sel, rw, topk, scale) ----
  * x bf16 [R][K]; wt fp32 [E][K] (the transposed gate); bias fp32 [E] or NULL (selection only); logits fp32 scratch
  * of hmoe_router_scratch_bytes(R, E) bytes; ctr unused (kept for the argument position); sel int64 [R][topk]; rw f16
- * [R][topk] = f16(a * scale / (sum a + 1e-20)); xh optional f16 [R][K] copy of x for hmoe_moe4_forward(xf = 1).
- * Logits in fp32 with one fixed summation order (bit-reproducible): 8 segments of K/8, each the in-order sum from 0
- * of 32-element fmaf chains (k ascending, from 0), the segment sums added in order from 0. Sigmoid, keys and weights
- * follow exl3_router.py:94-127 with the exp of include/hmoe_rng.h. R >= 1, E <= 256, topk <= 8, K % 256 == 0. */
+ * [R][topk] = f16(a * scale / (sum a + 1e-20)); xh optional f16 [R][K] copy of x for hmoe_moe4_forward(xf =
+ * HMOE_XF_F16). Logits in fp32 with one fixed summation order (bit-reproducible): 8 segments of K/8, each the in-order
+ * sum from 0 of 32-element fmaf chains (k ascending, from 0), the segment sums added in order from 0. Sigmoid, keys and
+ * weights follow exl3_router.py:94-127 with the exp of include/hmoe_rng.h. R >= 1, E <= 256, topk <= 8, K % 256 == 0.
+ * Scratch: R <= 16 rows use R x 256 fp32 (the reference's [8, 256] logits buffer, exl3_router.py:180, serves R <= 8),
+ * more rows 8 x R x 256 (one plane per segment). */
 size_t hmoe_router_scratch_bytes(int R, int E);
 int hmoe_router_fused(const void* x, const float* wt, const float* bias, float* logits, int* ctr, int64_t* sel,
                       uint16_t* rw, int R, int K, int E, int topk, float scale, void* xh, void* stream);
 
 /* ---- decode: runtime/tier/moe4/moe4.cu:828-895 moe4_forward ----
- * x [R][H] bf16 (xf = 0) or its f16 copy (xf = 1, as the router writes it); sel int64 [R][8]; rw f16 [R][8];
+ * x [R][H] bf16 (xf = HMOE_XF_BF16) or fp16 (xf = HMOE_XF_F16, e.g. the router's copy); xf = HMOE_XF_FRAG (the
+ * reference's fragment-order x) returns HMOE_ERR_ARG; sel int64 [R][8]; rw f16 [R][8];
  * picks with sel - lo in [0, n_hot) run, tables indexed by sel - lo hold I4G128 codes (gate/up [I][H], down [H][I])
  * and their scales; y fp32 [R][H] is accumulated into. sh_gw / sh_uw / sh_dw: the shared expert as F16T (gate/up
  * [I][H], down [H][I]) or NULL; sh_gs / sh_us / sh_ds must be NULL (the reference's int8 row scales; F16T has none).
@@ -128,7 +138,8 @@ int hmoe_finish_bf16(float* y, int rows, uint16_t* out, void* stream);
  * sel int64 [T][topk], rw f16 [T][topk]; window [lo, lo + n). Outputs: counts int32 [n], tok/eid int32 [T*topk],
  * wt fp32 [T*topk], inv int32 [T*topk] (position of each flat pick, -1 outside the window), rbt int32 [nrb_max][4]
  * rows {expert, first pick, picks, 0} with bm rows per block (balance as pick_groups), meta int32 [4] = {npos, nrb,
- * 0, 0}. work: scratch of hmoe_dispatch_work_bytes(T, topk, n) bytes. nrb_max = hmoe_dispatch_nrb_max(T*topk, n, bm). */
+ * 0, 0}. work: scratch of hmoe_dispatch_work_bytes(T, topk, n) bytes. nrb_max = hmoe_dispatch_nrb_max(T*topk, n, bm).
+ * bm in [1, 256] (the reference uses 64 for moe4p and 256, balanced, for moe4t: tier_split.py:417,449,457). */
 size_t hmoe_dispatch_work_bytes(int T, int topk, int n);
 int hmoe_dispatch_nrb_max(int npos_max, int n, int bm);
 int hmoe_dispatch(const int64_t* sel, const uint16_t* rw, int T, int topk, int lo, int n, int bm, int balance,
@@ -137,13 +148,15 @@ int hmoe_dispatch(const int64_t* sel, const uint16_t* rw, int T, int topk, int l
 
 /* ---- prefill: runtime/tier/moe4/moe4p.cu:217-245 moe4p_forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar,
  * d, out) ----
- * x bf16 [T][H] (xf = 0) or its f16 copy (xf = 1, as router_fused writes it); tok int32 [npos] (token of each pick),
+ * x bf16 [T][H] (xf = HMOE_XF_BF16) or fp16 (xf = HMOE_XF_F16, e.g. router_fused's copy; HMOE_XF_FRAG is refused);
+ * tok int32 [npos] (token of each pick),
  * eid int32 [npos] (not read: the expert of a row block is in
- * rbt), wt fp32 [npos]; rbt int32 [nrb][4] rows {expert (relative to the tables), first pick, picks <= 128, 0};
+ * rbt), wt fp32 [npos]; rbt int32 [nrb][4] rows {expert (relative to the tables), first pick, picks <= 256, 0} (a
+ * block of more than 128 picks runs as two halves in one workgroup; the dispatch's bm is at most 256);
  * tables (n_tab entries) as in hmoe_moe4_forward; ar f16 [ps + T][I] and d fp32 [ps + T][H] scratch
  * (hmoe_moe4p_scratch_bytes); gu (256-byte aligned, hmoe_moe4p_scratch_bytes(0) bytes): the f16 copy of x [T][H]
- * when xf = 0, then with the shared expert its fp32 gate | up sums [T][2I] and the library GEMMs' workspace (NULL
- * allowed when xf = 1 and there is no shared expert); out fp32 [T][H] accumulated into. meta: NULL, or the device
+ * when x is bf16, then with the shared expert its fp32 gate | up sums [T][2I] and the library GEMMs' workspace (NULL
+ * allowed for fp16 x without the shared expert); out fp32 [T][H] accumulated into. meta: NULL, or the device
  * {npos, nrb} written by hmoe_dispatch (then npos / nrb are the static maxima the grids are sized for). inv: NULL
  * (picks added with atomics, as p4_fin_kernel) or the dispatch's inverse map (each token's picks added in top-k
  * order: deterministic). sh_*: the shared expert as row-major f16 (gate [I][H], up [I][H], down [H][I]) or NULL
@@ -156,6 +169,37 @@ int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid, const floa
                        const int64_t* us, const int64_t* ds, float* gu, uint16_t* ar, float* d, float* out, int ps,
                        const int* meta, const int* inv, int T, int topk, const void* sh_gw, const void* sh_uw,
                        const void* sh_dw, int xf, void* stream);
+
+/* ---- long prefill: runtime/tier/moe4/moe4t.cu:490-524 moe4t_scratch(device, npos) / moe4t_forward(x, tok, eid, wt,
+ * rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out) ----
+ * As hmoe_moe4p_forward for the chunks the reference sends to moe4t (more than 2048 rows, tier_split.py:427-462,543):
+ * row blocks of up to 256 picks (hmoe_dispatch with bm = 256 and balance, as pick_groups(..., 256, True)), and the
+ * down GEMM adds its rows into out[tok] itself (fp32 atomics, the reference's fused epilogue, moe4t.cu:514-516): no d
+ * round trip and no combine launch, so the order of the adds into out varies run to run. Scratch
+ * (hmoe_moe4t_scratch_bytes(which, npos)): gu fp32 [2][npos][I] (unused, kept for the argument), ar f16 [npos][I],
+ * d fp32 [1][npos][H] (holds the f16 copy of x when x is bf16; the reference gathers the picks' rows into it).
+ * T: rows of x and out; meta as in moe4p (the device plan's {npos, nrb}, or NULL); no shared expert (the reference
+ * runs it apart at prefill: hmoe_shared_forward). npos = 0 is a no-op (moe4t.cu:508). */
+size_t hmoe_moe4t_scratch_bytes(int which, int npos);      /* which: 0 gu, 1 ar, 2 d */
+int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid, const float* wt, const int* rbt, int npos,
+                       int nrb, int n_tab, const int64_t* gw, const int64_t* uw, const int64_t* dw, const int64_t* gs,
+                       const int64_t* us, const int64_t* ds, float* gu, uint16_t* ar, float* d, float* out, int ps,
+                       const int* meta, int T, int xf, void* stream);
+/* runtime/tier/moe4/moe4t.cu:476-488 moe4t_gemm(xs, rbt, w0, w1, out, down), the test entry: one grouped GEMM over
+ * row blocks of <= 256 picks whose inputs are rows p of xs f16 [rows][K]. Gate/up shape (down = 0, K = H): out fp32
+ * [2][ps][I] = the gate (w0, s0) and up (w1, s1) sums; down shape (down = 1, K = I): out fp32 [ps][H] (w0, s0). The
+ * reference writes raw sums and applies its per-row scale later; with group-128 scales there is no row factor, so
+ * the sums here include the group scales. */
+int hmoe_moe4t_gemm(const void* xs, int rows, const int* rbt, int nrb, int n_tab, const int64_t* w0, const int64_t* w1,
+                    const int64_t* s0, const int64_t* s1, float* out, int ps, int down, void* stream);
+
+/* ---- the shared expert alone over a chunk (this build's addition: the reference runs it through the model's own
+ * shared-expert MLP at prefill, runtime/tier/tier_split.py:548-560, next to moe4t): out fp32 [T][H] += down(silu(gate
+ * x) * up x), x bf16 / fp16 [T][H] (xf as above), the weights row-major f16 (gate [I][H], up [I][H], down [H][I]);
+ * work: hmoe_shared_work_bytes(T) bytes, 256-byte aligned. Every output element is added once: deterministic. */
+size_t hmoe_shared_work_bytes(int T);
+int hmoe_shared_forward(const void* x, int T, const void* sh_gw, const void* sh_uw, const void* sh_dw, void* work,
+                        float* out, int xf, void* stream);
 
 /* ---- residual + RMSNorm between layers: runtime/tier/cn.cu:48-103 (combine_norm) restated for fp32 weights ----
  * r fp32 [R][H] residual += a (a fp32 [R][H] or NULL; a is zeroed after use), xn = bf16(r * rsqrt(mean r^2 + eps) * w)
@@ -177,39 +221,52 @@ int hmoe_norm_router(const float* h, const float* norm_w, float eps, int R, cons
  * A pool of host threads serves decode jobs of <= HMOE_CPU_MAXR rows from a mailbox: the cold experts of the job's
  * layer (ids in [lo, lo + n)) with q8_0 activations and int4 x int8 dot products (the arithmetic of cpuband.cpp with
  * bf16 group-128 scales), the fp32 partial into out. The mailbox is any host memory the pool can read; for the GPU
- * hand-off it must be pinned and device-mapped (hipHostMalloc, mapped + coherent). Protocol: the poster fills rows,
- * layer, sel, rw and x, then sets pending = 1 (release); the pool computes, writes out and err (0; 1 for a row count
- * outside [1, 8], 2 for a layer it does not hold, with out zero), then sets pending = 0 (release). Jobs are
- * serialised by the flag, so a job does not overlap the next. */
+ * hand-off it must be pinned and device-mapped (hipHostMalloc, mapped + coherent).
+ * Protocol (generation numbers, as cpuband.cpp:117-136,221 with ISSUE gen / CPU_DONE = gen): a poster may post when
+ * done == issue (the last job finished); it fills rows, layer, sel, rw and x, then stores issue = issue + 1 (release;
+ * 0 is skipped on wrap-around). Each pool thread remembers the last generation it served and runs a job when issue
+ * differs from it; after the job's last barrier the pool writes out and err (0; 1 for a row count outside [1, 8], 2
+ * for a layer it does not hold, with out zero) and stores done = the job's generation (release). A waiter waits for
+ * done == the generation it posted: a stale value of done (an older job, or any other number) never satisfies it.
+ * With HMOE_CPU_SKIP=1 in the environment at pool start, jobs are acknowledged with a zero partial (the timing
+ * diagnostic of cpuband.cpp:40,249). */
 #define HMOE_CPU_MAXR 8        /* rows per CPU job (cpuband.cpp:7, 154: MAXR = 8) */
 typedef struct hmoe_cpu_mailbox
 {
-    int32_t pending;                              /* 1 = a job is posted, 0 = done (own 128-byte line) */
-    int32_t pad0[31];
-    int32_t rows, layer, err;                     /* job header, written before pending */
+    uint32_t issue;                               /* generation of the last posted job (own 128-byte line) */
+    uint32_t pad0[31];
+    uint32_t done;                                /* generation of the last finished job (own 128-byte line) */
+    uint32_t pad1[31];
+    int32_t rows, layer, err;                     /* job header, written before issue */
     int32_t gpu_err;                              /* sticky, set by the GPU side: 1 a collect's wait ran out (partial
-                                                     not added), 2 a hand-off found the pool busy (job not posted);
-                                                     the host reads and clears it */
-    int32_t pad1[28];
+                                                     not added), 2 a hand-off found the pool busy (job not posted;
+                                                     later collects add nothing while it is set); the host reads and
+                                                     clears it */
+    int32_t pad2[28];
     int64_t sel[HMOE_CPU_MAXR * HMOE_TOPK];       /* global expert ids [rows][8] */
     uint16_t rw[HMOE_CPU_MAXR * HMOE_TOPK];       /* f16 routing weights [rows][8] */
     uint16_t x[HMOE_CPU_MAXR * HMOE_H];           /* bf16 rows */
     float out[HMOE_CPU_MAXR * HMOE_H];            /* fp32 partial [rows][H] */
 } hmoe_cpu_mailbox;
-/* start the pool (threads >= 1, pinned to cores first_core + t when first_core >= 0) on a mailbox; one pool per process */
+/* start the pool (threads >= 1, pinned to cores first_core + t when first_core >= 0) on a mailbox; one pool per process.
+ * The pool serves the jobs posted after it starts (it takes the mailbox's issue as already served). A test hook:
+ * HMOE_CPU_HOLD="t,usec" in the environment at start makes pool thread t sleep usec after each job before it looks
+ * for the next (the window in which a fast poster re-posts), in steps that watch for hmoe_cpu_stop. */
 int hmoe_cpu_start(hmoe_cpu_mailbox* mb, int threads, int first_core);
 /* the cold experts of a layer, host memory: q[3 e + {0, 1, 2}] the row-major int4 codes (cpuband.cpp:3-4: [N][K/2],
  * low nibble first) of gate [I][H], up [I][H], down [H][I] of cold expert e (id lo + e), s[...] their bf16 [N][K/128]
- * scales; the pool keeps the pointers (the caller keeps the memory alive) */
+ * scales; the pool keeps the pointers (the caller keeps the memory alive). Every pointer is checked before the layer
+ * changes, so a refused call leaves the pool's layers as they were. Only while no job is in flight. */
 int hmoe_cpu_add_layer(int layer, int lo, int n, const uint8_t* const* q, const uint16_t* const* s);
 int hmoe_cpu_stats(long long* jobs, long long* picks);
 int hmoe_cpu_stop(void);
-/* the GPU side of a job, one kernel each, capturable in a hipGraph. hmoe_cpu_submit: x bf16 [R][H], sel, rw (device,
- * 16-byte aligned) copied into the mailbox, rows / layer / err written, then pending = 1 with a system-scope release
- * (runtime/tier/moe4/moe4.cu:719-738 moe4_handoff_kernel). hmoe_cpu_collect: waits for pending == 0 and adds out into
- * y fp32 [R][H] (runtime/tier/tier_split.py:577-644 tier_combine, the graph form's spinning combine). Both waits are
- * bounded (2 s of wall clock); past the bound the kernel sets gpu_err and returns. The mailbox must come from
- * hmoe_cpu_mailbox_alloc (or be otherwise device-mapped). */
+/* the GPU side of a job, one kernel each, capturable in a hipGraph. hmoe_cpu_submit: waits for done == issue (the
+ * previous job finished), copies x bf16 [R][H], sel, rw (device, 16-byte aligned) into the mailbox, writes rows /
+ * layer / err, then issue + 1 with a system-scope release (runtime/tier/moe4/moe4.cu:719-738 moe4_handoff_kernel).
+ * hmoe_cpu_collect: waits for done == issue (the generation the submit before it posted, read from the mailbox) and
+ * adds out into y fp32 [R][H] (runtime/tier/tier_split.py:577-644 tier_combine, the graph form's spinning combine).
+ * Both waits are bounded (2 s of wall clock); past the bound the kernel sets gpu_err and returns; a collect adds
+ * nothing while gpu_err is set. The mailbox must come from hmoe_cpu_mailbox_alloc (or be otherwise device-mapped). */
 int hmoe_cpu_submit(hmoe_cpu_mailbox* mb, const void* x, const int64_t* sel, const uint16_t* rw, int R, int layer,
                     void* stream);
 int hmoe_cpu_collect(hmoe_cpu_mailbox* mb, float* y, int R, void* stream);

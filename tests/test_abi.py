@@ -173,3 +173,70 @@ def test_load_reference_int4_files(tmp_path):
             assert np.array_equal(s2, np.repeat(O.f32_to_bf16(rs)[:, None], K // 128, 1)), (e, m)
     with pytest.raises(RuntimeError):
         tier.load_reference_int4(str(tmp_path), 5, [4], "cpu")
+
+
+# ---- boundary: argument meanings the reference gives and this build cannot honour are refused, not misread ----------
+
+def _fake(n=1 << 16):
+    """a host buffer whose address stands in for every pointer argument (never dereferenced: the calls below are
+    refused by their argument checks before any launch)"""
+    return np.zeros(n, np.uint8)
+
+
+def test_fragment_order_x_is_refused():
+    """xf = 1 means x in B-fragment order in the reference (moe4.cu:826); the C ABI refuses it instead of reading it
+    as row-major, and the Python mirror does the same; an fp16 tensor with xf = 0 (the reference's call) is fp16"""
+    import torch
+    from hecate_amd import moe4
+    L = _lib.lib()
+    b = _fake()
+    p = b.ctypes.data
+    common = [p, p, p, 1, 8, p, p, p, p, p, p, p, p, p, p, p, p, 0, 0, 0, None, None, None, None, None, None]
+    assert L.hmoe_moe4_forward(*common, _lib.XF_FRAG, None) == 1
+    assert b"fragment-order" in L.hmoe_last_error()
+    assert L.hmoe_moe4_gate_up(p, p, p, 1, 8, p, p, p, p, p, p, p, 0, 0, None, None, _lib.XF_FRAG, None) == 1
+    assert b"fragment-order" in L.hmoe_last_error()
+    pf = [p, p, p, p, p, 8, 1, 8] + [p] * 10 + [8, None, None, 1, 8, None, None, None]
+    assert L.hmoe_moe4p_forward(*pf, _lib.XF_FRAG, None) == 1 and b"fragment-order" in L.hmoe_last_error()
+    assert L.hmoe_moe4t_forward(p, p, p, p, p, 8, 1, 8, *([p] * 10), 8, None, 1, _lib.XF_FRAG, None) == 1
+    assert L.hmoe_moe4_forward(*common, 3, None) == 1                       # unknown flags too
+    x16 = torch.zeros(1, 6144, dtype=torch.float16)
+    assert _lib.xf_of(x16, 0) == _lib.XF_F16 and _lib.xf_of(x16.bfloat16(), 0) == _lib.XF_BF16
+    with pytest.raises(RuntimeError, match="fragment"):
+        _lib.xf_of(x16, 1)
+    with pytest.raises(RuntimeError, match="bf16 or fp16"):
+        _lib.xf_of(x16.float(), 0)
+    with pytest.raises(RuntimeError, match="device"):
+        moe4.forward(x16, *([torch.zeros(1, 8, dtype=torch.int64)] * 2), 8, *([torch.zeros(8, dtype=torch.int64)] * 6),
+                     *([torch.zeros(1)] * 5), torch.zeros(1, 6144), 0, 0, 0)
+
+
+def test_router_scratch_is_the_reference_buffer_up_to_8_rows():
+    """exl3_router.py:180 allocates logits fp32 [8, 256] for 2..8 rows: that buffer is large enough here too"""
+    L = _lib.lib()
+    ref_bytes = 8 * 256 * 4
+    for R in range(1, 9):
+        assert L.hmoe_router_scratch_bytes(R, 256) <= ref_bytes
+    assert L.hmoe_router_scratch_bytes(16, 256) == 16 * 256 * 4
+    assert L.hmoe_router_scratch_bytes(17, 256) == 8 * 17 * 256 * 4          # the large path's segment planes
+
+
+def test_dispatch_block_size_is_bounded():
+    """row blocks of up to 256 picks (the reference's moe4t bm) are accepted; larger ones are refused, because the
+    grouped GEMMs run a block as at most two 128-pick halves"""
+    L = _lib.lib()
+    b = _fake()
+    p = b.ctypes.data
+    args = lambda bm: (p, p, 4, 8, 0, 256, bm, 1, p, p, p, p, p, p, 64, p, p, None)
+    assert L.hmoe_dispatch(*args(257)) == 1 and b"bm 257" in L.hmoe_last_error()
+    assert L.hmoe_dispatch(*args(0)) == 1
+    assert L.hmoe_dispatch_nrb_max(8 * 8192, 256, 256) == 256 + 8 * 8192 // 256
+
+
+def test_moe4t_no_picks_is_a_no_op():
+    """moe4t.cu:508 returns when no pick reaches the tier: npos = 0 returns before any check or launch"""
+    L = _lib.lib()
+    assert L.hmoe_moe4t_forward(*([None] * 5), 0, 0, 0, *([None] * 10), 0, None, 0, 0, None) == 0
+    assert L.hmoe_moe4t_scratch_bytes(1, 100) == 100 * 2048 * 2
+    assert L.hmoe_moe4t_scratch_bytes(2, 100) == 100 * 6144 * 4
+    assert L.hmoe_shared_forward(None, 0, None, None, None, None, None, 0, None) == 0

@@ -110,8 +110,7 @@ def test_cpu_tier_bad_jobs(cold):
         _, err = t.wait()
         assert err == 0
         t.mb.rows, t.mb.err = 9, 0                   # a row count past the mailbox
-        t.mb.pending = 1
-        t._rows = 1
+        t.raise_issue(1)
         _, err = t.wait()
         assert err == 1
     finally:
@@ -164,3 +163,103 @@ def test_cpu_tier_entry_points_reject_bad_arguments(cold):
     finally:
         t.close()
     assert L.hmoe_cpu_stop() == 0                                # (stopping twice is harmless)
+
+
+# ---- the hand-off protocol under forced timing (tools/dev/test_grace_picks.py:95-152 style, host-driven, no GPU) ----
+
+def test_immediate_repost_while_a_worker_is_held(hl, cold, monkeypatch):
+    """pool thread 1 sleeps after every job (HMOE_CPU_HOLD), so each next job is posted while it has not yet looked
+    for work: with a 0/1 flag that thread could take the re-raised flag for the job it had just finished and deadlock
+    the pool; with generations every job runs once, in order, with the oracle's bits"""
+    monkeypatch.setenv("HMOE_CPU_HOLD", "1,30000")
+    t = start(cold, 4)
+    try:
+        for j in range(6):
+            R = 1 + j % 3
+            x = x_rows(900 + j, R)
+            sel, rw = picks(R, 40 + j)
+            g = t.post(x, sel, rw, 0)
+            out, err = t.wait(timeout=20.0)
+            assert err == 0 and int(t.mb.done) == g
+            assert np.array_equal(out.view(np.uint32), oracle_q8(hl, x, sel, rw).view(np.uint32)), j
+        assert t.stats()[0] == 6
+    finally:
+        t.close()
+
+
+def test_stale_done_never_ends_a_wait(hl, cold, monkeypatch):
+    """a value of done that is not the posted generation (here a larger stale one, which a '>=' wait would take, as
+    the reference's reset of CPU_DONE to 0 guards against, tier_split.py:128-138) does not end the wait: the waiter
+    gets the job's own result once the pool finishes it"""
+    monkeypatch.setenv("HMOE_CPU_HOLD", "1,300000")        # job 2 waits ~0.3 s for thread 1
+    t = start(cold, 3)
+    try:
+        x = x_rows(60, 2)
+        sel, rw = picks(2, 60)
+        t.post(x, sel, rw, 0)
+        t.wait(timeout=20.0)
+        x2 = x_rows(61, 3)
+        sel2, rw2 = picks(3, 61)
+        g = t.post(x2, sel2, rw2, 0)
+        t.mb.done = g + 7                                    # stale, larger than the posted generation
+        out, err = t.wait(timeout=20.0)
+        assert err == 0 and int(t.mb.done) == g
+        assert np.array_equal(out.view(np.uint32), oracle_q8(hl, x2, sel2, rw2).view(np.uint32))
+    finally:
+        t.close()
+
+
+def test_stop_during_a_stuck_job(cold, monkeypatch):
+    """a job that cannot finish (one thread held for 30 s, the others waiting for it at the job's first barrier) does
+    not keep hmoe_cpu_stop from returning: barriers and the hold watch the stop flag"""
+    import time
+    monkeypatch.setenv("HMOE_CPU_HOLD", "1,30000000")
+    t = start(cold, 3)
+    x = x_rows(70, 1)
+    sel, rw = picks(1, 70)
+    t.post(x, sel, rw, 0)
+    t.wait(timeout=20.0)                                     # job 1 done; thread 1 now held
+    g = t.post(x, sel, rw, 0)                                # job 2: stuck at its first barrier
+    time.sleep(0.2)
+    assert int(t.mb.done) != g
+    t0 = time.perf_counter()
+    t.close()
+    assert time.perf_counter() - t0 < 5.0
+
+
+def test_skip_mode_acknowledges_with_zero(cold, monkeypatch):
+    """HMOE_CPU_SKIP=1 (cpuband.cpp:40,249's EXL3_TIER_CPU_SKIP): jobs are acknowledged with a zero partial"""
+    monkeypatch.setenv("HMOE_CPU_SKIP", "1")
+    t = start(cold, 2)
+    try:
+        x = x_rows(80, 4)
+        sel, rw = picks(4, 80)
+        t.mb.out[0] = 5.0
+        t.post(x, sel, rw, 0)
+        out, err = t.wait(timeout=20.0)
+        assert err == 0 and not out.any()
+    finally:
+        t.close()
+
+
+def test_add_layer_refusal_leaves_the_layer(hl, cold):
+    """a call with a null matrix pointer is refused before the layer changes: the pool still serves the old one"""
+    import ctypes
+    from hecate_amd import _lib
+    t = start(cold, 2)
+    try:
+        n = 2
+        q = (ctypes.c_void_p * (3 * n))()
+        s = (ctypes.c_void_p * (3 * n))()
+        keep = np.zeros(16, np.uint8)
+        for i in range(3 * n):
+            q[i] = s[i] = keep.ctypes.data
+        q[4] = None
+        assert _lib.lib().hmoe_cpu_add_layer(0, 0, n, q, s) != 0 and b"null matrix" in _lib.lib().hmoe_last_error()
+        x = x_rows(90, 2)
+        sel, rw = picks(2, 90)
+        t.post(x, sel, rw, 0)
+        out, err = t.wait(timeout=20.0)
+        assert err == 0 and np.array_equal(out.view(np.uint32), oracle_q8(hl, x, sel, rw).view(np.uint32))
+    finally:
+        t.close()

@@ -8,10 +8,11 @@ import pytest
 import torch
 
 import pyoracle as O
-from hecate_amd import moe4, moe4p, router, synth, tier
+import torchref
+from hecate_amd import moe4, moe4p, moe4t, router, synth, tier
 from hecate_amd.stack import DecodeStack
 from hecate_amd._lib import call, ptr
-from hostref import HostLayer, x_rows, parity, MAX_ABS, MEAN_REL, H, I, E
+from hostref import HostLayer, x_rows, parity, parity_ulp, MAX_ABS, MEAN_REL, H, I, E
 
 pytestmark = pytest.mark.gpu
 
@@ -368,6 +369,30 @@ def test_dispatch_bit_exact(dev):
         assert np.array_equal(rbt_py, rbt_ref)
 
 
+def check_all_rows(lay, hl, x, xn, y, sel_ref, rw_ref, sample=12, seed=0, with_shared=True):
+    """every row of y fp32 [T, H] against the torch fp32 reference on the same selection, and that reference pinned to
+    the oracle's exact mode on `sample` rows (the first and last among them); returns the bounds"""
+    T = x.shape[0]
+    sel = torch.from_numpy(sel_ref).to(x.device)
+    rw = torch.from_numpy(rw_ref.view(np.int16)).to(x.device).view(torch.float16)
+    ref = torchref.moe_rows(lay, x, sel, rw, with_shared).cpu().numpy()
+    extra = np.random.default_rng(seed).choice(T, max(min(T, sample) - 2, 0), replace=False)
+    rows = np.unique(np.concatenate([[0, T - 1], extra]))
+    orc = O.moe(0, xn[rows], sel_ref[rows], rw_ref[rows], hl.table(sel_ref[rows], lay.lo), lay.lo, lay.n_hot,
+                hl.shared if with_shared else None, threads=16)
+    pa, pr = parity(ref[rows], orc)
+    ma, mr = parity(y, ref)
+    log(f"  torch reference vs oracle on rows {rows.tolist()}: max|d| {pa:.3e} mean-rel {pr:.3e}")
+    log(f"  all {T} rows vs the torch reference: max|d| {ma:.3e} mean-rel {mr:.3e}")
+    # the reference shares the f16 weight rounding of the kernels and differs from the oracle by it alone
+    assert pa <= MAX_ABS / 2 and pr <= MEAN_REL / 2
+    assert ma <= MAX_ABS and mr <= MEAN_REL
+    # and per row: no row may hide a large error inside the chunk's mean
+    row_rel = np.abs(y - ref).mean(axis=1) / np.maximum(np.abs(ref).mean(axis=1), 1e-30)
+    assert row_rel.max() <= 4 * MEAN_REL, int(row_rel.argmax())
+    return ma, mr
+
+
 def test_prefill_parity(dev):
     T = 2048
     log("prefill T=2048")
@@ -383,18 +408,14 @@ def test_prefill_parity(dev):
     assert np.array_equal(sel, sel_ref) and np.array_equal(rw, rw_ref)
     counts = np.bincount(sel_ref.ravel(), minlength=E)
     log(f"  tokens per expert: min {counts.min()} mean {counts.mean():.1f} max {counts.max()}")
-    # the fp32 output before rounding (recompute into a zeroed accumulator, then compare a sample of rows)
+    # the fp32 output before rounding (recompute into a zeroed accumulator), every row
     y = pf.y[:T]
     y.zero_()
     lay.prefill_experts(x, y)
     yh = y.cpu().numpy()
     y.zero_()
     torch.cuda.synchronize()
-    rows = np.random.default_rng(0).choice(T, 12, replace=False)
-    ref = hl.moe(xn[rows], sel_ref[rows], rw_ref[rows])
-    ma, mr = parity(yh[rows], ref)
-    log(f"  sampled rows max|d| {ma:.3e} mean-rel {mr:.3e}")
-    assert ma <= MAX_ABS and mr <= MEAN_REL
+    check_all_rows(lay, hl, x, xn, yh, sel_ref, rw_ref)
 
 
 def test_decode_bits_do_not_depend_on_the_grid(dev):
@@ -468,7 +489,7 @@ def test_prefill_replays_in_a_graph(dev):
 def test_prefill_ragged(dev, T):
     """prefill chunks that are not a multiple of the 128-row block (the shared expert's last block partial, experts
     with one or two picks): routing bit-exact, the router's f16 copy of x exact, the fp32 output of the f16 input path
-    within tolerance on sampled rows (the first and last among them), and the bf16 output its rounding"""
+    within tolerance on every row, and the bf16 output its rounding"""
     log(f"prefill T={T}")
     lay = gpu_layer("c2", dev, layer=0, bias_sigma=0.001, max_rows=2048)
     hl = host_layer(0, bias_sigma=0.001)
@@ -488,8 +509,203 @@ def test_prefill_ragged(dev, T):
     y.zero_()
     torch.cuda.synchronize()
     assert np.array_equal(u16(out), O.f32_to_bf16(yh))
-    extra = np.random.default_rng(T).choice(T, max(min(T, 12) - 2, 0), replace=False)
-    rows = np.unique(np.concatenate([[0, T - 1], extra]))
-    ma, mr = parity(yh[rows], hl.moe(xn[rows], sel_ref[rows], rw_ref[rows]))
-    log(f"  rows {rows.tolist()}: max|d| {ma:.3e} mean-rel {mr:.3e}")
-    assert ma <= MAX_ABS and mr <= MEAN_REL
+    check_all_rows(lay, hl, x, xn, yh, sel_ref, rw_ref, seed=T)
+
+
+def test_prefill_blocks_of_256_picks(dev):
+    """moe4p on a dispatch plan with bm = 256 (balanced, as moe4t's pick_groups): blocks of more than 128 picks run as
+    two halves in one workgroup; every row within tolerance of the torch reference, and the same routing"""
+    T = 2048
+    log("prefill T=2048 with 256-pick blocks (moe4p)")
+    lay = gpu_layer("c2", dev, layer=0, bias_sigma=0.001, max_rows=2048)
+    hl = host_layer(0, bias_sigma=0.001)
+    x = synth.gen_x(2, T, dev)
+    xn = u16(x)
+    pb = tier.PrefillBuffers(T, 8, 0, lay.n_hot, 256, dev, bm=256)
+    router.router_fused(x, lay.wg, lay.bias, pb.logits, lay.ctr, pb.sel, pb.rw, 8, 2.5, pb.xh)
+    pb.run(pb.sel, pb.rw, balance=True)
+    torch.cuda.synchronize()
+    rbt = pb.rbt[:int(pb.meta[1].item())].cpu().numpy()
+    log(f"  {len(rbt)} row blocks, picks per block: max {rbt[:, 2].max()}, blocks over 128: {(rbt[:, 2] > 128).sum()}")
+    gq, uq, dq, gs, us, ds = lay.bank.tables()
+    y = torch.zeros((T, H), dtype=torch.float32, device=dev)
+    moe4p.forward(pb.xh, pb.tok, pb.eid, pb.wt, pb.rbt, gq, uq, dq, gs, us, ds, *pb.scr, y, inv=pb.inv, meta=pb.meta,
+                  topk=8, shared=lay.shared_rows(), npos=pb.F, nrb=pb.nrb_max)
+    torch.cuda.synchronize()
+    sel_ref, rw_ref = hl.route(xn)
+    assert np.array_equal(pb.sel.cpu().numpy(), sel_ref)
+    check_all_rows(lay, hl, x, xn, y.cpu().numpy(), sel_ref, rw_ref, seed=256)
+    del pb
+
+
+@pytest.mark.parametrize("T", [4096, 8192])
+def test_long_prefill_moe4t(dev, T):
+    """chunks above 2048 rows on moe4t (tier_split.py:543): 256-pick balanced blocks, the down GEMM adding into the
+    output with atomics, the shared expert apart; routing bit-exact, every row within tolerance"""
+    log(f"long prefill T={T} (moe4t)")
+    lay = gpu_layer("c2", dev, layer=0, bias_sigma=0.001, max_rows=2048)
+    hl = host_layer(0, bias_sigma=0.001)
+    x = synth.gen_x(5000 + T, T, dev)
+    xn = u16(x)
+    out = lay.prefill(x).clone()
+    torch.cuda.synchronize()
+    pf = lay._pf
+    assert pf.long and pf.bm == 256
+    sel_ref, rw_ref = hl.route(xn)
+    assert np.array_equal(pf.sel[:T].cpu().numpy(), sel_ref) and np.array_equal(u16(pf.rw[:T]), rw_ref)
+    counts = np.bincount(sel_ref.ravel(), minlength=E)
+    rbt = pf.rbt[:int(pf.meta[1].item())].cpu().numpy()
+    assert np.array_equal(rbt, O.pick_groups(counts, 256, True))
+    log(f"  picks per expert {counts.min()}..{counts.max()}, {len(rbt)} blocks of up to {rbt[:, 2].max()} picks")
+    y = pf.y[:T]
+    y.zero_()
+    lay.prefill_experts(pf.xh[:T], y)
+    yh = y.cpu().numpy()
+    y.zero_()
+    torch.cuda.synchronize()
+    # (the atomic adds make the last bits of a run order-dependent: bf16 out within one ulp of this run's rounding)
+    ob = O.bf16_to_f32(u16(out))
+    assert np.abs(ob - O.bf16_to_f32(O.f32_to_bf16(yh))).max() <= 2 ** -7 * max(np.abs(yh).max(), 1.0)
+    check_all_rows(lay, hl, x, xn, yh, sel_ref, rw_ref, seed=T)
+    lay._pf = None
+    torch.cuda.empty_cache()
+
+
+def test_moe4t_gemm_entry(dev):
+    """moe4t.gemm (moe4t.cu:476-488): one grouped GEMM over given pick inputs, gate/up shape (both sums) and down
+    shape, against torch fp32 GEMMs on the dequantised weights of each block's expert"""
+    import torch.nn.functional as F
+    log("moe4t.gemm")
+    lay = gpu_layer("c2", dev, layer=0, bias_sigma=0.001, max_rows=2048)
+    g = torch.Generator().manual_seed(3)
+    counts = np.array([200, 0, 17, 256, 1, 130], np.int64)          # blocks of 200, 17, 256, 1, 65 + 65 picks
+    rbt = O.pick_groups(counts, 256, True)
+    npos = int(counts.sum())
+    xs = torch.randn((npos, H), generator=g).half().to(dev)
+    act = (torch.randn((npos, I), generator=g) * 0.1).half().to(dev)
+    gq, uq, dq, gs, us, ds = lay.bank.tables()
+    rb = torch.from_numpy(rbt).to(dev)
+    o_gu = moe4t.gemm(xs, rb, gq, uq, torch.zeros((2, npos, I), device=dev), 0, gs, us)
+    o_d = moe4t.gemm(act, rb, dq, None, torch.zeros((1, npos, H), device=dev), 1, ds)
+    torch.cuda.synchronize()
+    starts = np.concatenate([[0], np.cumsum(counts)])
+    for e in np.nonzero(counts)[0]:
+        p0, p1 = int(starts[e]), int(starts[e + 1])
+        wg = moe4.dequant(lay.bank.view("gate_q", e), lay.bank.view("gate_s", e), I, H).float()
+        wu = moe4.dequant(lay.bank.view("up_q", e), lay.bank.view("up_s", e), I, H).float()
+        wd = moe4.dequant(lay.bank.view("down_q", e), lay.bank.view("down_s", e), H, I).float()
+        for got, ref in ((o_gu[0, p0:p1], F.linear(xs[p0:p1].float(), wg)), (o_gu[1, p0:p1], F.linear(xs[p0:p1].float(), wu)),
+                         (o_d[0, p0:p1], F.linear(act[p0:p1].float(), wd))):
+            d = (got - ref).abs()
+            assert d.max().item() <= 2e-3 * max(ref.abs().max().item(), 1.0), (e, d.max().item())
+
+
+def test_combine_with_partials(dev):
+    """moe4.combine with both partials (moe4.cu:700-717): f = ((f + y) + o) + o2 in fp32, bit for bit, and y zeroed;
+    with one partial NULL the order is (f + y) + o"""
+    log("combine with o / o2")
+    g = torch.Generator().manual_seed(11)
+    R = 5
+    f, y, o, o2 = [(torch.randn((R, H), generator=g) * s).to(dev) for s in (1.0, 0.5, 0.3, 0.2)]
+    f0 = f.clone(); y0 = y.clone()
+    moe4.combine(f, o, y, R, o2)
+    torch.cuda.synchronize()
+    fh, yh, oh, o2h = (t.cpu().numpy() for t in (f0, y0, o, o2))
+    ref = ((fh + yh) + oh) + o2h
+    assert np.array_equal(f.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    assert not y.any()
+    f = f0.clone(); y = y0.clone()
+    moe4.combine(f, o, y, R)
+    torch.cuda.synchronize()
+    assert np.array_equal(f.cpu().numpy().view(np.uint32), ((fh + yh) + oh).view(np.uint32)) and not y.any()
+    with pytest.raises(RuntimeError, match="DONE"):
+        moe4.combine(f, o, y, R, o2, 1234)
+
+
+def test_router_with_the_reference_logits_buffer(dev):
+    """router_fused with the reference's logits scratch fp32 [8, 256] (exl3_router.py:180) for 2..8 rows"""
+    hl = host_layer(0)
+    wg = torch.from_numpy(hl.wg).to(dev); b = torch.from_numpy(hl.bias).to(dev)
+    logits = torch.zeros((8, 256), dtype=torch.float32, device=dev)
+    ctr = torch.zeros(1, dtype=torch.int32, device=dev)
+    for R in (2, 8):
+        x = x_rows(300 + R, R)
+        xt = torch.from_numpy(x.view(np.int16)).to(dev).view(torch.bfloat16)
+        sel = torch.empty((R, 8), dtype=torch.int64, device=dev); rw = torch.empty((R, 8), dtype=torch.float16, device=dev)
+        router.router_fused(xt, wg, b, logits, ctr, sel, rw, 8, 2.5)
+        torch.cuda.synchronize()
+        sel_ref, rw_ref = hl.route(x)
+        assert np.array_equal(sel.cpu().numpy(), sel_ref) and np.array_equal(u16(rw), rw_ref)
+
+
+def test_decode_fp16_input_as_the_reference_passes_it(dev):
+    """moe4.forward with fp16 x and xf=0 (the reference's call, tier_split.py:563-567) reads fp16: the result equals
+    the router's f16 copy passed the same way, and the bf16 x path gives the same bits (f16(bf16 x) is exact)"""
+    R = 3
+    lay = gpu_layer("c2", dev, layer=0, bias_sigma=0.001, max_rows=2048)
+    x = synth.gen_x(31, R, dev)
+    lay.route(x)
+    gq, uq, dq, gs, us, ds = lay.bank.tables()
+    outs = []
+    for xin in (lay.xh[:R], x):
+        y = torch.zeros((R, H), dtype=torch.float32, device=dev)
+        moe4.forward(xin, lay.sel[:R], lay.rw[:R], lay.n_hot, gq, uq, dq, gs, us, ds, *lay.scr, y, 0, 0, 0, xf=0)
+        outs.append(y)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    with pytest.raises(RuntimeError, match="fragment"):
+        moe4.forward(x, lay.sel[:R], lay.rw[:R], lay.n_hot, gq, uq, dq, gs, us, ds, *lay.scr, outs[0], 0, 0, 0, xf=1)
+
+
+def test_stack_16_layers_b4(dev):
+    """config 4 at its stated size: 16 layers (about 80 GB of int4 experts), B = 4, residual + RMSNorm between them.
+    Eager (unfused) step: the norm bit-exact and routing bit-exact on every layer against the oracle (on the GPU's own
+    layer inputs), layer outputs within tolerance on layers 0, 7 and 15; the fused step gives the same bits; its
+    captured hipGraph replays them three times with eager work between. The synthetic layers' codes (uniform in
+    [-8, 7], mean -0.5) and positive group scales give every weight row a negative mean, so each layer's output carries
+    a common-mode term that the residual accumulates: from layer 2 on the outputs are O(100-1000), where 2e-2 is finer
+    than bf16 itself, so the max-abs bound reads "<= 2e-2 or <= 1 bf16 ulp of the reference" (elementwise)"""
+    log("stack of 16 layers, R=4")
+    _LAYERS.clear()
+    torch.cuda.empty_cache()
+    R, L = 4, 16
+    layers = [synth.make_layer(l, dev) for l in range(L)]
+    ws = [synth.gen_normal(synth.key(synth.SEED, l, synth.KIND["NORM_W"]), H, dev, 1.0, 0.02) for l in range(L)]
+    st = DecodeStack(layers, ws, R)
+    x = synth.gen_x(4, R, dev)
+    st.x.copy_(x)
+    tr = []
+    h_eager = st.step(trace=tr, fused=False).clone()
+    torch.cuda.synchronize()
+    h_prev = x.float().cpu().numpy()
+    y_prev = None
+    U = []
+    for l, (r_after, xn, y, sel, rw) in enumerate(tr):
+        r_ref, xn_ref = O.residual_rmsnorm(h_prev, y_prev, ws[l].cpu().numpy(), 1e-5)
+        assert np.array_equal(r_after.cpu().numpy().view(np.uint32), r_ref.view(np.uint32)), l
+        assert np.array_equal(u16(xn), xn_ref), l
+        hl = HostLayer(l, shared=l in (0, 7, 15))
+        sel_ref, rw_ref = hl.route(xn_ref)
+        assert np.array_equal(sel.cpu().numpy(), sel_ref) and np.array_equal(u16(rw), rw_ref), l
+        U.append(len(np.unique(sel_ref)))
+        if l in (0, 7, 15):
+            ref = hl.moe(xn_ref, sel_ref, rw_ref)
+            ma, mr = parity(y.cpu().numpy(), ref)
+            mu, _ = parity_ulp(y.cpu().numpy(), ref)
+            log(f"  layer {l}: max|ref| {np.abs(ref).max():.3e} max|d| {ma:.3e} (bound units {mu:.3f}) mean-rel {mr:.3e}")
+            assert mu <= 1.0 and mr <= MEAN_REL
+        h_prev, y_prev = r_after.cpu().numpy(), y.cpu().numpy()
+    log(f"  distinct experts per layer: {U}")
+    assert np.array_equal(h_eager.cpu().numpy(), (tr[-1][0] + tr[-1][2]).cpu().numpy())
+    h_f = st.step(fused=True).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(h_f, h_eager)
+    st.capture(fused=True)
+    for rep in range(3):
+        st.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(st.h, h_eager), f"replay {rep}"
+        junk = torch.randn(1 << 20, device=dev).sum()           # eager work between replays
+        torch.cuda.synchronize()
+    del st, layers
+    torch.cuda.empty_cache()

@@ -339,3 +339,14 @@ def test_rmsnorm_fp64_and_exact_order():
     rmf = np.float32(np.float32(1) / np.sqrt(np.float32(part[0] / np.float32(H)) + np.float32(1e-5), dtype=np.float32))
     exp = O.f32_to_bf16(((vf * rmf).astype(np.float32) * w).astype(np.float32))
     assert np.array_equal(xn[0], exp)
+
+
+def test_bf16_ulp_is_the_spacing_of_bf16():
+    """the ulp used by the tolerance's "<= 1 bf16 ulp" reading equals the distance to the next bf16 number"""
+    from hostlayer import bf16_ulp
+    rng = np.random.default_rng(3)
+    v = (rng.standard_normal(2000) * np.exp2(rng.integers(-20, 20, 2000))).astype(np.float32)
+    b = O.f32_to_bf16(v)
+    up = (b & 0x8000) | ((b & 0x7fff) + 1)                     # next magnitude (sign kept)
+    spacing = np.abs(O.bf16_to_f32(up).astype(np.float64) - O.bf16_to_f32(b).astype(np.float64))
+    assert np.array_equal(bf16_ulp(O.bf16_to_f32(b)), spacing)
