@@ -25,6 +25,8 @@ SIGNATURES = {
     "hmoe_moe4_scratch_bytes": (sz, [i32]),
     "hmoe_moe4_forward": (i32, [P, P, P, i32, i32, P, P, P, P, P, P, P, P, P, P, P, P, i32, i32, i32,
                                 P, P, P, P, P, P, i32, P]),
+    "hmoe_moe4_noalloc_bytes": (sz, []),
+    "hmoe_moe4_forward_noalloc": (i32, [P, P, P, i32, i32, P, P, P, P, P, P, P, i32, P, P, P, i32, P]),
     "hmoe_moe4_gate_up": (i32, [P, P, P, i32, i32, P, P, P, P, P, P, P, i32, i32, P, P, i32, P]),
     "hmoe_moe4_down": (i32, [P, P, i32, i32, P, P, P, P, P, P, i32, i32, P, P]),
     "hmoe_moe_decode_layer": (i32, [P, P, P, i32, i32, f32, P, P, P, i32, i32, i32, P, P, P, P, P, P, P, P, P, P, P,

@@ -32,6 +32,7 @@
 #include "hmoe_dev.h"
 
 #include <atomic>
+#include <mutex>
 
 namespace hmoe {
 
@@ -748,6 +749,63 @@ extern "C" int hmoe_moe4_forward(const void* x, const int64_t* sel, const uint16
     int rc = check(a);
     if (rc) return rc;
     HMOE_REQUIRE(sel && rw && y, "moe4_forward: null buffer");
+    return run_decode(a, 15, (hipStream_t) stream);
+}
+
+// ---- the allocation-free decode op: hmoe_moe4_forward with its workspace (act, part count, part partials) in one
+// file-scope device array, for callers that cannot allocate (under graph capture, in a serving loop that forbids it).
+// Each device holds its own copy of the array; its address is taken once per device with the device current, and
+// only that address (never the array's name, which in host code is a stand-in, not a device address) reaches a kernel.
+namespace hmoe {
+constexpr size_t NA_ACT = (size_t) ACT_SLOTS * MAXR * I * 2;           // act f16 [134][16][2048]
+constexpr size_t NA_CTR = (size_t) CTR_WORDS * 4;                      // ctr: the part count
+constexpr size_t NA_Y32 = (size_t) MAX_PARTS * MAXR * H * 4;           // y32: part partials [33][16][6144]
+constexpr size_t NA_BYTES = NA_ACT + NA_CTR + NA_Y32;                  // 21,762,048 bytes
+static_assert(NA_ACT % 256 == 0 && NA_CTR % 256 == 0, "each piece stays 256-byte aligned");
+}  // namespace hmoe
+
+static __device__ __align__(256) uint8_t scratch[hmoe::NA_BYTES];
+
+namespace hmoe {
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64];
+
+// the device address of `scratch` on the current device (looked up on the first call there)
+static int scratch_ptr(uint8_t** out)
+{
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return set_error(HMOE_ERR_HIP, "moe4_forward_noalloc: current device");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev])
+    {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return set_error(HMOE_ERR_HIP, "moe4_forward_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = (uint8_t*) g_scratch_ptr[dev];
+    return HMOE_OK;
+}
+}  // namespace hmoe
+
+extern "C" size_t hmoe_moe4_noalloc_bytes(void) { return NA_BYTES; }
+
+extern "C" int hmoe_moe4_forward_noalloc(const void* x, const int64_t* sel, const uint16_t* rw, int R, int n_hot,
+                                         const int64_t* gate_w, const int64_t* up_w, const int64_t* down_w,
+                                         const int64_t* gate_s, const int64_t* up_s, const int64_t* down_s, float* y,
+                                         int lo, const void* sh_gw, const void* sh_uw, const void* sh_dw, int xf,
+                                         void* stream)
+{
+    HMOE_REQUIRE(R >= 1 && R <= MAXR, "moe4_forward_noalloc: rows %d beyond the static workspace (at most %d rows, %zu "
+                 "bytes)", R, MAXR, NA_BYTES);
+    uint8_t* ws = nullptr;
+    if (int rc = scratch_ptr(&ws)) return rc;
+    DecodeArgs a = forward_args(x, sel, rw, R, n_hot, gate_w, up_w, down_w, gate_s, up_s, down_s, ws + 0,
+                                (int*) (ws + NA_ACT), (float*) (ws + NA_ACT + NA_CTR), y, 0, lo, sh_gw, sh_uw, sh_dw, xf);
+    int rc = check(a);
+    if (rc) return rc;
+    HMOE_REQUIRE(sel && rw && y, "moe4_forward_noalloc: null buffer");
     return run_decode(a, 15, (hipStream_t) stream);
 }
 

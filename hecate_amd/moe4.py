@@ -91,3 +91,19 @@ def finish_bf16(y, rows, out):
     on_device("finish_bf16", y, out)
     call("hmoe_finish_bf16", ptr(y), int(rows), ptr(out), stream_of(y.device))
     return out
+
+
+def forward_noalloc(x, sel, rw, n_hot, gate_w, up_w, down_w, gate_s, up_s, down_s, y, lo=0, sh_gw=0, sh_uw=0, sh_dw=0,
+                    xf=0):
+    """forward without workspace arguments (hmoe_moe4_forward_noalloc): the library's static per-device workspace, no
+    allocation anywhere in the call; calls that overlap on one GPU race"""
+    R = x.shape[0]
+    on_device("moe4.forward_noalloc", x, sel, rw, gate_w, up_w, down_w, gate_s, up_s, down_s, y)
+    fmt = xf_of(x, xf)
+    _req(x.is_contiguous() and x.shape[-1] == H, "x layout")
+    _req(sel.dtype == torch.int64 and sel.is_contiguous() and sel.shape == (R, TOPK), "selection int64 [R, 8]")
+    _req(rw.dtype == torch.float16 and rw.is_contiguous() and rw.shape == (R, TOPK), "routing weights f16 [R, 8]")
+    _req(y.dtype == torch.float32 and y.is_contiguous() and y.shape[-1] == H and y.numel() >= R * H, "y fp32 [R, H]")
+    call("hmoe_moe4_forward_noalloc", ptr(x), ptr(sel), ptr(rw), R, int(n_hot), ptr(gate_w), ptr(up_w), ptr(down_w),
+         ptr(gate_s), ptr(up_s), ptr(down_s), ptr(y), int(lo), _addr(sh_gw), _addr(sh_uw), _addr(sh_dw), fmt,
+         stream_of(x.device))

@@ -101,6 +101,18 @@ int hmoe_moe4_forward(const void* x, const int64_t* sel, const uint16_t* rw, int
                       void* act, float* gu32, int* ctr_a, float* y32, int* ctr_b, float* y, int blocks, int blocks_a,
                       int lo, const void* sh_gw, const void* sh_uw, const void* sh_dw, const void* sh_gs,
                       const void* sh_us, const void* sh_ds, int xf, void* stream);
+/* hmoe_moe4_forward without workspace arguments: no counterpart in the reference. For callers that cannot allocate
+ * (code under hipGraph capture, serving loops or harnesses that forbid hipMalloc): act, the part count and the part
+ * partials live in one static device array of hmoe_moe4_noalloc_bytes() bytes (21,762,048: sized for R <= 16 rows;
+ * more rows return HMOE_ERR_ARG), which each GPU the library runs on holds until the process ends. The call allocates
+ * nothing and frees nothing. Every call on a GPU shares that GPU's array, so calls that overlap on one GPU (other
+ * streams, other threads) race; nothing in it needs clearing (each launch reads only what the call wrote). The
+ * other arguments are those of hmoe_moe4_forward, with blocks = 0. */
+size_t hmoe_moe4_noalloc_bytes(void);
+int hmoe_moe4_forward_noalloc(const void* x, const int64_t* sel, const uint16_t* rw, int R, int n_hot,
+                              const int64_t* gate_w, const int64_t* up_w, const int64_t* down_w,
+                              const int64_t* gate_s, const int64_t* up_s, const int64_t* down_s, float* y, int lo,
+                              const void* sh_gw, const void* sh_uw, const void* sh_dw, int xf, void* stream);
 /* the two phases of hmoe_moe4_forward, for callers that time or schedule them apart (this build's addition):
  * gate_up writes act (with the shared expert: also its fp32 gate and up sums, in act) and, in act, the step's routing
  * record (distinct expert count and the local expert of each act slot); down adds into y (ctr_b carries its part
