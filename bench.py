@@ -3,13 +3,16 @@
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only WORKLOAD]
 
-Headline (`value`): the 16-row decode step (8 requests + 8 draft rows, Zipf(1.1) expert popularity): one MoE layer
-(router + routed int4 experts + shared expert + bf16 output) per step, in tokens/s, the steps captured in one hipGraph
-and replayed (eager launches reported beside it). Steps cycle over 6 seeded
-layers and 64 seeded inputs so consecutive steps stream different weights (the working set of a step is far above
-the 256 MB last-level cache, as in a real decode pass through 75+ layers). Extras: decode at 1 and 8 rows, the
-2048-token prefill chunk, the 176-resident partial tier at 1/4/8 rows, the same split with the other 80 experts on the
-host-CPU tier, and the 16-layer hipGraph step at 4 rows.
+Headline (`value`): BASELINE.json's config 0, the decode step at B = 1: one MoE layer (router + top-8 of 256 int4
+g128 experts + bf16 shared expert + bf16 output) per step, in tokens/s, the timed steps captured in one hipGraph and
+replayed (eager launches reported beside it). Steps cycle over 6 seeded layers and 64 seeded inputs so consecutive
+steps stream different weights (a step's working set is far above the 256 MB last-level cache, as in a real decode
+pass through 75+ layers). Extras: decode at 8 rows and at 16 rows with Zipf(1.1) popularity (config 1), the
+2048-token prefill chunk (config 2) and an 8192-token chunk on the long-prefill op, the 176-resident partial tier at
+1/4/8 rows (config 3), the same split with the other 80 experts on the host-CPU tier, the 16-layer hipGraph step at
+4 rows (config 4), and a near-tie audit of the selections. cpu_baseline: the reference's CPU expert path (cpuband.cpp
+restated: the pinned host pool of hecate_amd/csrc/cputier.cpp) with the router and the shared expert on the same
+cores, per config, on bounded samples.
 One JSON line on stdout; progress on stderr.
 """
 import argparse
@@ -134,6 +137,8 @@ def decode_workload(torch, synth, R, steps, warmup, zipf, dev, n_layers=6, n_x=6
 
 
 def prefill_workload(torch, synth, steps, warmup, dev, T=2048):
+    """per step: one chunk of T tokens through a layer (router, device dispatch plan, grouped GEMMs of the routed
+    experts, shared expert, combine, bf16 out), alternating 2 layers and 2 inputs; T > 2048 runs the long-prefill op"""
     import numpy as np
     t0 = time.perf_counter()
     layers = [synth.make_layer(l, dev, bias_sigma=0.001, max_rows=T) for l in range(2)]
@@ -147,7 +152,8 @@ def prefill_workload(torch, synth, steps, warmup, dev, T=2048):
     flop = T * 8 * 3 * 2 * 2048 * 6144 + T * 3 * 2 * 2048 * 6144 + T * 2 * 256 * 6144
     bytes_step = 256 * EXPERT_BYTES + SHARED_BYTES + ROUTER_BYTES + 2 * T * H * 2
     counts = np.bincount(layers[0]._pf.sel[:T].cpu().numpy().ravel(), minlength=256)
-    res = {"tokens": T, "ms_per_chunk": step_s * 1e3, "tok_per_s": T / step_s, "flop": flop,
+    res = {"tokens": T, "op": "moe4t" if T > 2048 else "moe4p", "ms_per_chunk": step_s * 1e3, "tok_per_s": T / step_s,
+           "flop": flop,
            "tflops": flop / step_s / 1e12, "mfma_frac": flop / step_s / 1e12 / MFMA_PEAK_TFLOPS,
            "hbm_frac": bytes_step / step_s / 1e9 / HBM_PEAK_GBS,
            "picks_per_expert": [int(counts.min()), float(counts.mean()), int(counts.max())]}
@@ -243,9 +249,12 @@ def graph_workload(torch, synth, steps, warmup, dev, n_layers=16, R=4):
     U = np.array([len(torch.unique(l.sel[:R])) for l in layers], np.float64)
     step_s = el / steps
     b = float(np.sum(U * EXPERT_BYTES + SHARED_BYTES + ROUTER_BYTES + R * H * 12))
+    # (the synthetic codes, uniform in [-8, 7], have mean -0.5 and the group scales are positive, so every weight row
+    # has a negative mean: each layer's output carries a common-mode term that the residual accumulates, and from the
+    # third layer on the 4 rows' normalised inputs share it and pick mostly the same experts)
     res = {"layers": n_layers, "rows": R, "us_per_step": step_s * 1e6, "us_per_token": step_s * 1e6 / R,
-           "distinct_experts_per_layer": float(U.mean()), "bytes_per_step": b, "hbm_gbs": b / step_s / 1e9,
-           "hbm_frac": b / step_s / 1e9 / HBM_PEAK_GBS}
+           "distinct_experts_per_layer": float(U.mean()), "distinct_experts_by_layer": [int(u) for u in U],
+           "bytes_per_step": b, "hbm_gbs": b / step_s / 1e9, "hbm_frac": b / step_s / 1e9 / HBM_PEAK_GBS}
     del st, layers
     torch.cuda.empty_cache()
     return res
@@ -264,41 +273,235 @@ def copy_workload(torch, steps, warmup, dev, nbytes=1 << 30):
     return res
 
 
-def cpu_baseline(budget_s=12.0):
-    """the CPU expert path (oracle q8_0 mode: runtime/tier/cpuband.cpp restated) on the 16-row Zipf step of layer 0,
-    as two 8-row jobs (cpuband caps a job at 8 rows) after the CPU router, timed on this host's cores"""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+def near_tie_audit(torch, synth, dev):
+    """rows whose 8th and 9th selection scores (sigmoid(l) + bias) are closer than a different fp32 summation order of
+    the logits could move them: the reference's fused router adds chunk partials in whatever order its atomics land
+    (exl3_router.py:66-71), and it notes that its routers can resolve such near-ties differently (exl3_router.py:5-6).
+    Bound per expert: 2^-24 sqrt(K) sum_k |x_k w_ek| (the statistical size of the rounding difference between two
+    summation orders over K terms) times sigmoid'(l) = a (1 - a); a row is a near-tie when the gap is below the sum of
+    its two experts' bounds"""
     import numpy as np
-    import pyoracle as O
-    from hostlayer import HostLayer, x_rows
-    from hecate_amd import synth
-    threads = max(1, min(16, os.cpu_count() or 1))
-    hl = HostLayer(0, bias=synth.zipf_bias(layer=0))
-    comp, steps = 0.0, 0
-    for i in range(64):
-        x = x_rows(i, 16)
-        t0 = time.perf_counter()
-        sel, rw = O.router(x, hl.wg, hl.bias)
-        t1 = time.perf_counter()
-        tab = hl.table(sel)                           # host weight generation, not timed
-        t2 = time.perf_counter()
-        for j in (0, 8):
-            O.moe(1, x[j:j + 8], sel[j:j + 8], rw[j:j + 8], tab, 0, 256, hl.shared, threads=threads)
-        t3 = time.perf_counter()
-        comp += (t1 - t0) + (t3 - t2)
-        steps += 1
-        if comp >= budget_s:
-            break
+    torch.backends.cuda.matmul.allow_tf32 = False
+    K = H
+    out = {}
+    cases = (("config0_b1", {}, 1, 64, 0), ("config1_b16_zipf", {"bias": synth.zipf_bias()}, 16, 16, 1000),
+             ("config2_prefill_2048", {"bias_sigma": 0.001}, 2048, 1, 2))
+    for name, kw, R, nx, tag0 in cases:
+        wg, b = synth.router_weights(0, dev, **kw)
+        rows = near = 0
+        worst = float("inf")
+        for i in range(nx):
+            x = synth.gen_x(tag0 + i, R, dev).float()
+            lg = x @ wg.t()
+            a = torch.sigmoid(lg)
+            sc = a + b
+            top = sc.topk(9, dim=1)
+            gap = top.values[:, 7] - top.values[:, 8]
+            mag = x.abs() @ wg.abs().t()
+            bound = 2.0 ** -24 * K ** 0.5 * mag * a * (1 - a)
+            bnd = bound.gather(1, top.indices[:, 7:8])[:, 0] + bound.gather(1, top.indices[:, 8:9])[:, 0]
+            rows += R
+            near += int((gap < bnd).sum().item())
+            worst = min(worst, float((gap / bnd).min().item()))
+        out[name] = {"rows": rows, "near_ties": near, "min_gap_over_bound": worst}
+    return out
+
+
+def cpu_cores(cap=16):
+    """the cores the CPU baseline runs on: the physical cores of the socket of this process's first allowed CPU, minus
+    the first 4 (the reference runs 60 workers from core 12 of 72, tier_split.py:35-36, leaving the first cores to
+    the serving process), capped at the box's CPU share for one GPU; returns (cores, description)"""
+    allowed = sorted(os.sched_getaffinity(0))
+    topo = {}
+    for c in allowed:
+        try:
+            with open(f"/sys/devices/system/cpu/cpu{c}/topology/physical_package_id") as f:
+                pkg = int(f.read())
+            with open(f"/sys/devices/system/cpu/cpu{c}/topology/core_id") as f:
+                core = int(f.read())
+        except (OSError, ValueError):
+            pkg, core = 0, c
+        topo[c] = (pkg, core)
+    sock = topo[allowed[0]][0]
+    seen, phys = set(), []
+    for c in allowed:
+        if topo[c][0] == sock and topo[c][1] not in seen:
+            seen.add(topo[c][1])
+            phys.append(c)
+    use = phys[4:] if len(phys) > 8 else phys
+    use = use[:cap]
     model = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
             model = next(ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name"))
     except Exception:
         pass
-    return {"value": 16 * steps / comp, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{steps} steps of the 16-row Zipf decode step of layer 0 (router + 2 x 8-row q8_0 jobs of the "
-                      f"restated cpuband path + fp32 shared expert), {comp:.1f} s of compute on {model}, "
-                      f"{threads} OpenMP threads"}
+    info = {"nproc": os.cpu_count(), "allowed_cpus": len(allowed), "cpu_model": model,
+            "physical_cores_in_socket": len(phys), "threads": len(use), "first_core": use[0],
+            "pinned": use == list(range(use[0], use[0] + len(use))),
+            "cap_reason": f"all physical cores of the socket minus 4, at most {cap} (the box's CPU share per GPU)"}
+    return use, info
+
+
+def cpu_baseline():
+    """the reference's CPU path timed on this host's cores: the routed experts on the pinned pool of
+    hecate_amd/csrc/cputier.cpp (cpuband.cpp's jobs of <= 8 rows: q8_0 activations, int4 x int8 dots), the router and
+    the shared expert (which the reference keeps on its GPU) through torch's CPU GEMMs (bf16 shared weights, fp32
+    accumulation) on the same number of threads after the pool has stopped. Per config, on bounded samples (weights generated on the host
+    for the experts the sampled inputs pick, not timed); config 2 has no CPU prefill in the reference (cpuband.cpp:7)
+    and is timed as its 8-row jobs, an extension"""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import pyoracle as O
+    from hostlayer import HostLayer, x_rows
+    from hecate_amd import synth
+    from hecate_amd.cpu_tier import CpuTier
+    cores, info = cpu_cores()
+    threads = len(cores)
+    t_setup = time.perf_counter()
+    cache = {}
+
+    def expert(layer, e):
+        k = (layer, e)
+        if k not in cache:
+            kk = lambda kind: synth.key(synth.SEED, layer, synth.KIND[kind], e)
+            cache[k] = {"gate_q": O.codes(kk("GATE_Q"), 2048, H), "gate_s": O.scales(kk("GATE_S"), 2048, H, synth.SIG_SCALE),
+                        "up_q": O.codes(kk("UP_Q"), 2048, H), "up_s": O.scales(kk("UP_S"), 2048, H, synth.SIG_SCALE),
+                        "down_q": O.codes(kk("DOWN_Q"), H, 2048), "down_s": O.scales(kk("DOWN_S"), H, 2048, synth.SIG_SCALE)}
+        return cache[k]
+
+    # the sampled jobs: (config, pool layer, rows of x, sel, rw) and the host layers they need
+    hl0 = HostLayer(0, shared=True)
+    hlz = HostLayer(0, bias=synth.zipf_bias(layer=0), shared=False)
+    hl2 = HostLayer(0, bias_sigma=0.001, shared=False)
+    perm = synth.popularity_order()[:176]
+    perm = list(perm) + [e for e in range(256) if e not in set(perm)]
+    hl3 = HostLayer(0, perm=perm, n_hot=176, shared=False)
+    x0 = [x_rows(i, 1) for i in range(8)]
+    jobs = {"config0_b1": [], "config1_b16_zipf": [], "config3_b1": [], "config3_b4": [], "config3_b8": [],
+            "config2_prefill_8row_jobs": []}
+    r_s = {}                                                 # router + shared time per config (oracle, after the pool)
+    for x in x0:
+        sel, rw = hl0.route(x)
+        jobs["config0_b1"].append((0, x, sel, rw))
+    x16 = x_rows(1000, 16)
+    sel, rw = hlz.route(x16)
+    jobs["config1_b16_zipf"] += [(0, x16[j:j + 8], sel[j:j + 8], rw[j:j + 8]) for j in (0, 8)]
+    for B in (1, 4, 8):
+        xb = np.concatenate(x0[:B])
+        sel, rw = hl3.route(xb)
+        jobs[f"config3_b{B}"].append((1, xb, sel, rw))
+    x2 = x_rows(2, 8)
+    sel, rw = hl2.route(x2)
+    jobs["config2_prefill_8row_jobs"].append((0, x2, sel, rw))
+    # config 4: the first 4 of the 16 layers of the B = 4 stack (layer l is pool layer 10 + l), the chain computed on
+    # the host with the oracle's q8_0 path between them so each layer's job sees its own inputs
+    stack = []
+    h = O.bf16_to_f32(x_rows(4, 4)).copy()
+    y = None
+    for l in range(4):
+        w = O.normal_f32(synth.key(synth.SEED, l, synth.KIND["NORM_W"]), H, 1.0, 0.02)
+        h, xn = O.residual_rmsnorm(h, y, w, 1e-5)
+        hl = hl0 if l == 0 else HostLayer(l, shared=True)
+        sel, rw = hl.route(xn)
+        stack.append((10 + l, xn, sel, rw, hl))
+        tab = O.ExpertTable([expert(l, e) if e in set(int(v) for v in sel.ravel()) else None for e in range(256)])
+        y = O.moe(1, xn, sel, rw, tab, 0, 256, hl.shared, threads=threads)
+    # the pool's layers: every needed expert generated; the window's other slots point at a generated one (never
+    # picked by the sampled jobs)
+    def pool_layer(layer, ids_needed, ids_of_local):
+        ex = {e: expert(layer, e) for e in ids_needed}
+        fill = ex[next(iter(ex))]
+        return [ex.get(ids_of_local[j], fill) for j in range(len(ids_of_local))]
+    need0 = set()
+    for cfg in ("config0_b1", "config1_b16_zipf", "config2_prefill_8row_jobs"):
+        for _, _, sel, _ in jobs[cfg]:
+            need0 |= {int(e) for e in sel.ravel()}
+    need3 = set()
+    for B in (1, 4, 8):
+        for _, _, sel, _ in jobs[f"config3_b{B}"]:
+            need3 |= {perm[int(e)] for e in sel.ravel() if int(e) < 176}
+    layers = {0: pool_layer(0, need0, list(range(256))), 1: pool_layer(0, need3, perm[:176])}
+    for (pl, xn, sel, rw, hl) in stack:
+        layers[pl] = pool_layer(pl - 10, {int(e) for e in sel.ravel()}, list(range(256)))
+    setup_s = time.perf_counter() - t_setup
+    log(f"[bench] cpu baseline: {len(cache)} experts generated in {setup_s:.1f} s, {threads} pool threads on cores "
+        f"{cores[0]}..{cores[-1]}")
+    # pool jobs, each run 3 times (the median kept)
+    tier = CpuTier(threads=threads, first_core=cores[0] if info["pinned"] else -1, mapped=False)
+    pool_s = {}
+    try:
+        for pl, ex in layers.items():
+            tier.add_layer(pl, 0, ex)
+
+        def run(pl, x, sel, rw):
+            best = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                tier.post(x, sel, rw, pl)
+                _, err = tier.wait()
+                best.append(time.perf_counter() - t0)
+                if err:
+                    raise RuntimeError(f"cpu baseline: job error {err}")
+            return float(np.median(best))
+        for cfg, js in jobs.items():
+            pool_s[cfg] = [run(*j) for j in js]
+        pool_s["config4_stack_b4"] = [run(pl, xn, sel, rw) for (pl, xn, sel, rw, _) in stack]
+    finally:
+        tier.close()
+
+    # router (fp32 logits, sigmoid + bias top-8) and shared expert (bf16 weights and activations, fp32 accumulation)
+    # through torch's CPU GEMMs on the same number of threads, the pool stopped
+    import torch
+    import torch.nn.functional as F
+    torch.set_num_threads(threads)
+    tw = {}
+
+    def cpu_weights(hl):
+        if id(hl) not in tw:
+            sh = None
+            if hl.shared is not None:
+                sh = [torch.from_numpy(m.view(np.int16)).view(torch.bfloat16) for m in hl.shared]
+            tw[id(hl)] = (torch.from_numpy(hl.wg), torch.from_numpy(hl.bias), sh)
+        return tw[id(hl)]
+
+    def router_shared(hl, x, with_shared=True):
+        wg, bias, sh = cpu_weights(hl)
+        xb = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16)
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            a = torch.sigmoid(F.linear(xb.float(), wg))
+            top = (a + bias).topk(8, dim=1)
+            sa = a.gather(1, top.indices)
+            rw = (sa * 2.5 / (sa.sum(1, keepdim=True) + 1e-20)).half()
+            if with_shared:
+                ys = F.linear(F.silu(F.linear(xb, sh[0])) * F.linear(xb, sh[1]), sh[2])
+        return time.perf_counter() - t0
+    r_s["config0_b1"] = [router_shared(hl0, x) for x in x0]
+    r_s["config1_b16_zipf"] = [router_shared(hl0, x16)]
+    for B in (1, 4, 8):
+        r_s[f"config3_b{B}"] = [router_shared(hl3, np.concatenate(x0[:B]), False)]
+    r_s["config2_prefill_8row_jobs"] = [router_shared(hl0, x2)]
+    r_s["config4_stack_b4"] = [router_shared(hl, xn) for (_, xn, _, _, hl) in stack]
+    res = {}
+    for cfg in pool_s:
+        p, r = float(np.sum(pool_s[cfg])), float(np.sum(r_s[cfg]))
+        rows = {"config0_b1": 8, "config1_b16_zipf": 16, "config3_b1": 1, "config3_b4": 4, "config3_b8": 8,
+                "config2_prefill_8row_jobs": 8, "config4_stack_b4": 4}[cfg]
+        n_steps = {"config0_b1": 8}.get(cfg, 1)
+        step = (p + r) / n_steps
+        if cfg == "config4_stack_b4":
+            step = step * 16 / 4                             # 4 of the 16 layers sampled
+        res[cfg] = {"us_per_step": step * 1e6, "tok_per_s": (rows / n_steps) / step,
+                    "pool_us": p / n_steps * 1e6, "router_shared_us": r / n_steps * 1e6}
+    res["config2_prefill_8row_jobs"]["ms_per_2048_chunk"] = res["config2_prefill_8row_jobs"]["us_per_step"] * 256 / 1e3
+    head = res["config0_b1"]
+    info.update({"setup_s": setup_s, "experts_generated": len(cache)})
+    return {"value": head["tok_per_s"], "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": (f"config 0 (B = 1): 8 tokens of layer 0 (one 1-row job of the restated cpuband path on the "
+                       f"pinned pool, the median of 3 runs, + router and bf16 shared expert on torch's CPU GEMMs) on "
+                       f"{info['cpu_model']}, {threads} threads from core {cores[0]}; per-config figures in configs"),
+            "configs": res, "host": info}
 
 
 def traffic_from_profiles(kernel):
@@ -316,8 +519,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default=None, choices=[None, "decode16", "decode1", "decode8", "prefill", "partial",
-                                                     "graph16", "copy", "tiered"])
+    ap.add_argument("--only", default=None, choices=[None, "decode1", "decode16", "decode8", "prefill", "prefill8k",
+                                                     "partial", "graph16", "copy", "tiered", "ties", "cpu"])
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the path would shard by "
@@ -330,18 +533,21 @@ def main():
     only = args.only
     extra = {}
     head = None
-    if only in (None, "decode16"):
-        head = decode_workload(torch, synth, 16, K, W, True, dev, tag0=1000)
-        log(f"[bench] decode16: {json.dumps(head)}")
     if only in (None, "decode1"):
-        extra["decode_b1"] = decode_workload(torch, synth, 1, K, W, False, dev, tag0=0)
-        log(f"[bench] decode1: {json.dumps(extra['decode_b1'])}")
+        head = decode_workload(torch, synth, 1, K, W, False, dev, tag0=0)
+        log(f"[bench] decode1: {json.dumps(head)}")
     if only in (None, "decode8"):
         extra["decode_b8"] = decode_workload(torch, synth, 8, K, W, False, dev, tag0=500)
         log(f"[bench] decode8: {json.dumps(extra['decode_b8'])}")
+    if only in (None, "decode16"):
+        extra["decode_b16_zipf"] = decode_workload(torch, synth, 16, K, W, True, dev, tag0=1000)
+        log(f"[bench] decode16: {json.dumps(extra['decode_b16_zipf'])}")
     if only in (None, "prefill"):
         extra["prefill_2048"] = prefill_workload(torch, synth, max(10, K // 10), max(2, W // 10), dev)
         log(f"[bench] prefill: {json.dumps(extra['prefill_2048'])}")
+    if only in (None, "prefill8k"):
+        extra["prefill_8192"] = prefill_workload(torch, synth, max(6, K // 30), 2, dev, T=8192)
+        log(f"[bench] prefill8k: {json.dumps(extra['prefill_8192'])}")
     if only in (None, "partial"):
         extra["partial_176"] = partial_workload(torch, synth, K, W, dev)
         log(f"[bench] partial: {json.dumps(extra['partial_176'])}")
@@ -351,25 +557,32 @@ def main():
     if only in (None, "tiered"):
         extra["tiered_176_cpu80"] = tiered_workload(torch, synth, max(20, K // 10), max(3, W // 4), dev)
         log(f"[bench] tiered: {json.dumps(extra['tiered_176_cpu80'])}")
+    if only in (None, "ties"):
+        extra["near_tie_audit"] = near_tie_audit(torch, synth, dev)
+        log(f"[bench] ties: {json.dumps(extra['near_tie_audit'])}")
     if only == "copy":
         extra["copy_1gib"] = copy_workload(torch, max(10, K // 10), 3, dev)
+    cpu = None
+    if (only is None and not args.no_cpu) or only == "cpu":
+        cpu = cpu_baseline()
+        log(f"[bench] cpu: {json.dumps(cpu)}")
     if head is None:
-        print(json.dumps({"extra": extra}))
+        print(json.dumps({"extra": extra, "cpu_baseline": cpu}))
         return
-    cpu = None if args.no_cpu else cpu_baseline()
     kb = head["kernels"]["B_gate_up"]
     roof = {"bound": "hbm", "kernel": "gu7_kernel (shared gate/up + top-8 selection + routed int4 gate/up + SwiGLU)",
             "achieved": kb["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": kb["gbs"] / HBM_PEAK_GBS,
             "traffic": traffic_from_profiles("gu7_kernel"), "algorithmic_bytes_per_launch": kb["algorithmic_bytes"],
-            "launch_us": kb["us"]}
-    extra["decode_b16"] = head
+            "launch_us": kb["us"], "layer_hbm_frac": head["hbm_frac"]}
+    extra["decode_b1"] = head
     line = {"metric": metric_name(), "value": head["tok_per_s"], "unit": "tok/s", "n_gpus": 1, "steps": K,
             "warmup": W, "ms_per_step": head["us_per_step"] / 1e3, "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "f16 (int4 weights, fp32 accumulation)", "data": "synthetic",
-            "config": {"workload": "decode_b16_zipf: one routed int4 MoE layer step (router + top-8 of 256 int4 g128 "
-                                   "experts + bf16 shared expert + bf16 out), 16 rows, Zipf(1.1) popularity",
-                       "rows": 16, "hidden": H, "intermediate": 2048, "experts": 256, "topk": 8,
-                       "us_per_token": head["us_per_token"], "hbm_gbs": head["hbm_gbs"]},
+            "config": {"workload": "config 0, decode_b1: one routed int4 MoE layer step (router + top-8 of 256 int4 g128 "
+                                   "experts + bf16 shared expert + bf16 out), 1 row",
+                       "rows": 1, "hidden": H, "intermediate": 2048, "experts": 256, "topk": 8,
+                       "us_per_token": head["us_per_token"], "hbm_gbs": head["hbm_gbs"],
+                       "bytes_per_token": head["bytes_per_step"]},
             "roofline": roof, "cpu_baseline": cpu, "extra": extra}
     print(json.dumps(line))
 

@@ -601,7 +601,8 @@ extern "C" size_t hmoe_moe4t_scratch_bytes(int which, int npos)
 extern "C" int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid, const float* wt, const int* rbt,
                                   int npos, int nrb, int n_tab, const int64_t* gw, const int64_t* uw, const int64_t* dw,
                                   const int64_t* gs, const int64_t* us, const int64_t* ds, float* gu, uint16_t* ar,
-                                  float* d, float* out, int ps, const int* meta, int T, int xf, void* stream)
+                                  float* d, float* out, int ps, const int* meta, int T, int xf, const int* inv,
+                                  int topk, void* stream)
 {
     (void) eid; (void) gu;
     if (npos == 0) return HMOE_OK;                                      // moe4t.cu:508: no pick, no work
@@ -612,6 +613,7 @@ extern "C" int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid,
     HMOE_REQUIRE(xf == HMOE_XF_BF16 || xf == HMOE_XF_F16, "moe4t_forward: xf must be HMOE_XF_BF16 (0) or HMOE_XF_F16 (2)");
     HMOE_REQUIRE(((uintptr_t) x & 15) == 0 && ((uintptr_t) ar & 15) == 0 && ((uintptr_t) out & 15) == 0 &&
                  ((uintptr_t) d & 15) == 0, "moe4t_forward: alignment");
+    HMOE_REQUIRE(!inv || (d && topk >= 1 && topk <= TOPK), "moe4t_forward: the ordered combine needs d and topk");
     hipStream_t st = (hipStream_t) stream;
     const _Float16* xh = (const _Float16*) x;
     if (xf == HMOE_XF_BF16)
@@ -627,11 +629,19 @@ extern "C" int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid,
         pgemm_kernel<false, 2, 2, 3><<<dim3(nrb, I / 128), PT, 0, st>>>(xh, tok, wt, rbt, nrb, meta, n_tab, gw, uw, gs,
                                                                              us, nullptr, nullptr, (_Float16*) ar,
                                                                              nullptr, T, 0);
-        pgemm_kernel<false, 1, 4, 2, EPI_FIN><<<dim3(nrb, H / 256), PT, 0, st>>>((const _Float16*) ar, tok, nullptr,
-                                                                                rbt, nrb, meta, n_tab, dw, nullptr, ds,
-                                                                                nullptr, nullptr, nullptr, nullptr,
-                                                                                nullptr, T, 0, out);
+        // (d held the f16 copy of x, which the gate/up GEMM has consumed by now: the down rows may overwrite it)
+        if (inv)
+            pgemm_kernel<false, 1, 4, 2><<<dim3(nrb, H / 256), PT, 0, st>>>((const _Float16*) ar, nullptr, nullptr,
+                                                                                   rbt, nrb, meta, n_tab, dw, nullptr,
+                                                                                   ds, nullptr, nullptr, nullptr, nullptr,
+                                                                                   d, T, 0);
+        else
+            pgemm_kernel<false, 1, 4, 2, EPI_FIN><<<dim3(nrb, H / 256), PT, 0, st>>>((const _Float16*) ar, tok, nullptr,
+                                                                                    rbt, nrb, meta, n_tab, dw, nullptr,
+                                                                                    ds, nullptr, nullptr, nullptr,
+                                                                                    nullptr, nullptr, T, 0, out);
     }
+    if (inv) pfin_kernel<<<T, 256, 0, st>>>(d, inv, topk, -1, out);
     return HMOE_LAUNCHED("moe4t_forward");
 }
 

@@ -22,9 +22,12 @@ def scratch(dev, npos):
             torch.empty((1, npos, H), dtype=torch.float32, device=dev)]
 
 
-def forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, meta=None, npos=None, nrb=None):
-    """moe4t.cu:498-524: out[tok] += routed experts of the sorted picks; x fp16 (as the reference) or bf16 [T, H]"""
-    on_device("moe4t", x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, meta)
+def forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, meta=None, npos=None, nrb=None, inv=None,
+            topk=8):
+    """moe4t.cu:498-524: out[tok] += routed experts of the sorted picks; x fp16 (as the reference) or bf16 [T, H].
+    inv (the dispatch's inverse map, this build's addition): each token adds its picks in top-k order (deterministic)
+    instead of the down GEMM's atomic adds"""
+    on_device("moe4t", x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, meta, inv)
     T = x.shape[0]
     if not (x.dim() == 2 and x.shape[1] == H and x.is_contiguous() and out.dtype == torch.float32
             and out.is_contiguous() and out.shape[-1] == H and out.numel() >= T * H and rbt.dim() == 2
@@ -38,7 +41,7 @@ def forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, meta=N
         raise RuntimeError(f"moe4t: scratch for {ps} picks, {npos} given")
     call("hmoe_moe4t_forward", ptr(x), ptr(tok), ptr(eid), ptr(wt), ptr(rbt), npos, nrb, gw.numel(), ptr(gw),
          ptr(uw), ptr(dw), ptr(gs), ptr(us), ptr(ds), ptr(gu), ptr(ar), ptr(d), ptr(out), ps, ptr(meta), T, xf_of(x),
-         stream_of(x.device))
+         ptr(inv), int(topk), stream_of(x.device))
 
 
 def gemm(xs, rbt, w0, w1, out, down, s0=None, s1=None):

@@ -169,6 +169,7 @@ class MoELayer:
         self.E = wg.shape[0]
         self.lo, self.n_hot = lo, bank.n if n_hot is None else n_hot
         self.topk, self.scale = topk, scale
+        self.deterministic = True      # long prefill: ordered per-token combine (False: moe4t's atomic epilogue)
         self.max_rows = max(max_rows, 16)
         dev = self.device
         self.logits, self.ctr = router.buffers(self.max_rows, dev, self.E)
@@ -245,7 +246,8 @@ class MoELayer:
             # tier_split.py:427-462: every routed expert on moe4t (256-pick balanced blocks, the down GEMM adding into
             # y), the shared expert apart
             moe4t.forward(x, pf.tok, pf.eid, pf.wt, pf.rbt, gq, uq, dq, gs, us, ds, *pf.scr, y, meta=pf.meta,
-                          npos=pf.F, nrb=pf.nrb_max)
+                          npos=pf.F, nrb=pf.nrb_max, inv=pf.inv[:T * self.topk] if self.deterministic else None,
+                          topk=self.topk)
             if with_shared and self.shared is not None:
                 moe4t.shared(x, *self.shared_rows(), pf.shw, y)
             return

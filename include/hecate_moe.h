@@ -185,9 +185,11 @@ int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid, const floa
 /* ---- long prefill: runtime/tier/moe4/moe4t.cu:490-524 moe4t_scratch(device, npos) / moe4t_forward(x, tok, eid, wt,
  * rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out) ----
  * As hmoe_moe4p_forward for the chunks the reference sends to moe4t (more than 2048 rows, tier_split.py:427-462,543):
- * row blocks of up to 256 picks (hmoe_dispatch with bm = 256 and balance, as pick_groups(..., 256, True)), and the
- * down GEMM adds its rows into out[tok] itself (fp32 atomics, the reference's fused epilogue, moe4t.cu:514-516): no d
- * round trip and no combine launch, so the order of the adds into out varies run to run. Scratch
+ * row blocks of up to 256 picks (hmoe_dispatch with bm = 256 and balance, as pick_groups(..., 256, True)). inv NULL:
+ * the down GEMM adds its rows into out[tok] itself (fp32 atomics, the reference's fused epilogue, moe4t.cu:514-516),
+ * so the order of the adds into out varies run to run; inv = the dispatch's inverse map (this build's addition, with
+ * topk): the down rows go to d and each token adds its picks in top-k order (deterministic, and cheaper on gfx950
+ * than scattered fp32 atomics). Scratch
  * (hmoe_moe4t_scratch_bytes(which, npos)): gu fp32 [2][npos][I] (unused, kept for the argument), ar f16 [npos][I],
  * d fp32 [1][npos][H] (holds the f16 copy of x when x is bf16; the reference gathers the picks' rows into it).
  * T: rows of x and out; meta as in moe4p (the device plan's {npos, nrb}, or NULL); no shared expert (the reference
@@ -196,7 +198,7 @@ size_t hmoe_moe4t_scratch_bytes(int which, int npos);      /* which: 0 gu, 1 ar,
 int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid, const float* wt, const int* rbt, int npos,
                        int nrb, int n_tab, const int64_t* gw, const int64_t* uw, const int64_t* dw, const int64_t* gs,
                        const int64_t* us, const int64_t* ds, float* gu, uint16_t* ar, float* d, float* out, int ps,
-                       const int* meta, int T, int xf, void* stream);
+                       const int* meta, int T, int xf, const int* inv, int topk, void* stream);
 /* runtime/tier/moe4/moe4t.cu:476-488 moe4t_gemm(xs, rbt, w0, w1, out, down), the test entry: one grouped GEMM over
  * row blocks of <= 256 picks whose inputs are rows p of xs f16 [rows][K]. Gate/up shape (down = 0, K = H): out fp32
  * [2][ps][I] = the gate (w0, s0) and up (w1, s1) sums; down shape (down = 1, K = I): out fp32 [ps][H] (w0, s0). The

@@ -198,7 +198,7 @@ def test_fragment_order_x_is_refused():
     assert b"fragment-order" in L.hmoe_last_error()
     pf = [p, p, p, p, p, 8, 1, 8] + [p] * 10 + [8, None, None, 1, 8, None, None, None]
     assert L.hmoe_moe4p_forward(*pf, _lib.XF_FRAG, None) == 1 and b"fragment-order" in L.hmoe_last_error()
-    assert L.hmoe_moe4t_forward(p, p, p, p, p, 8, 1, 8, *([p] * 10), 8, None, 1, _lib.XF_FRAG, None) == 1
+    assert L.hmoe_moe4t_forward(p, p, p, p, p, 8, 1, 8, *([p] * 10), 8, None, 1, _lib.XF_FRAG, None, 8, None) == 1
     assert L.hmoe_moe4_forward(*common, 3, None) == 1                       # unknown flags too
     x16 = torch.zeros(1, 6144, dtype=torch.float16)
     assert _lib.xf_of(x16, 0) == _lib.XF_F16 and _lib.xf_of(x16.bfloat16(), 0) == _lib.XF_BF16
@@ -236,7 +236,7 @@ def test_dispatch_block_size_is_bounded():
 def test_moe4t_no_picks_is_a_no_op():
     """moe4t.cu:508 returns when no pick reaches the tier: npos = 0 returns before any check or launch"""
     L = _lib.lib()
-    assert L.hmoe_moe4t_forward(*([None] * 5), 0, 0, 0, *([None] * 10), 0, None, 0, 0, None) == 0
+    assert L.hmoe_moe4t_forward(*([None] * 5), 0, 0, 0, *([None] * 10), 0, None, 0, 0, None, 8, None) == 0
     assert L.hmoe_moe4t_scratch_bytes(1, 100) == 100 * 2048 * 2
     assert L.hmoe_moe4t_scratch_bytes(2, 100) == 100 * 6144 * 4
     assert L.hmoe_shared_forward(None, 0, None, None, None, None, None, 0, None) == 0

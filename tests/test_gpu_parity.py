@@ -538,16 +538,23 @@ def test_prefill_blocks_of_256_picks(dev):
     del pb
 
 
-@pytest.mark.parametrize("T", [4096, 8192])
-def test_long_prefill_moe4t(dev, T):
-    """chunks above 2048 rows on moe4t (tier_split.py:543): 256-pick balanced blocks, the down GEMM adding into the
-    output with atomics, the shared expert apart; routing bit-exact, every row within tolerance"""
-    log(f"long prefill T={T} (moe4t)")
+@pytest.mark.parametrize("T,ordered", [(4096, False), (4096, True), (8192, True)])
+def test_long_prefill_moe4t(dev, T, ordered):
+    """chunks above 2048 rows on moe4t (tier_split.py:543): 256-pick balanced blocks, the shared expert apart; the
+    combine either in the down GEMM's epilogue (fp32 atomics, as the reference) or ordered per token through the
+    inverse map (repeat calls bit-identical); routing bit-exact, every row within tolerance"""
+    log(f"long prefill T={T} (moe4t, {'ordered' if ordered else 'atomic'} combine)")
     lay = gpu_layer("c2", dev, layer=0, bias_sigma=0.001, max_rows=2048)
     hl = host_layer(0, bias_sigma=0.001)
     x = synth.gen_x(5000 + T, T, dev)
     xn = u16(x)
-    out = lay.prefill(x).clone()
+    lay.deterministic = ordered
+    try:
+        out = lay.prefill(x).clone()
+        if ordered:
+            assert torch.equal(lay.prefill(x), out)
+    finally:
+        lay.deterministic = True
     torch.cuda.synchronize()
     pf = lay._pf
     assert pf.long and pf.bm == 256
@@ -559,7 +566,11 @@ def test_long_prefill_moe4t(dev, T):
     log(f"  picks per expert {counts.min()}..{counts.max()}, {len(rbt)} blocks of up to {rbt[:, 2].max()} picks")
     y = pf.y[:T]
     y.zero_()
-    lay.prefill_experts(pf.xh[:T], y)
+    lay.deterministic = ordered
+    try:
+        lay.prefill_experts(pf.xh[:T], y)
+    finally:
+        lay.deterministic = True
     yh = y.cpu().numpy()
     y.zero_()
     torch.cuda.synchronize()
