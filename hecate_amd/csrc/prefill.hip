@@ -128,8 +128,10 @@ struct PFetch
 // moe4t); down -> d fp32 rows (EPI_D) or added into out[tok] with fp32 atomics (EPI_FIN, moe4t.cu's down epilogue)
 enum { EPI_ACT = 0, EPI_RAW = 1, EPI_D = 2, EPI_FIN = 3 };
 
-template <bool DENSE, int NMAT, int NS, int D, int EPI = NMAT == 2 ? EPI_ACT : EPI_D>
-__global__ void __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(2))) pgemm_kernel(
+// NTT: 16-pick tiles per pass (8: 128 picks, 4 waves; 16: 256 picks, 8 waves, one pass for the long prefill's 256-pick
+// blocks, each dequantised weight fragment feeding twice the MFMAs); NWV waves, each staging two tiles
+template <bool DENSE, int NMAT, int NS, int D, int EPI = NMAT == 2 ? EPI_ACT : EPI_D, int NTT = 8, int NWV = 4>
+__global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) pgemm_kernel(
     const _Float16* __restrict__ xin, const int* __restrict__ tok, const float* __restrict__ wt,
     const int* __restrict__ rbt, int nrb, const int* __restrict__ meta, int n_tab,
     const int64_t* __restrict__ w0, const int64_t* __restrict__ w1, const int64_t* __restrict__ s0,
@@ -142,25 +144,27 @@ __global__ void __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(2))) pg
     constexpr int NOUT = NMAT == 2 ? I : H;
     constexpr int KG = K / 128, KS = K / 32;
     static_assert(KG % D == 0, "the ring depth divides the k groups");
-    static_assert(NS * NMAT == 4, "four weight fragments per wave and k step");
+    static_assert(NS * NMAT * NTT == 32, "32 accumulator tiles per wave (4 fragments x 8 tiles or 2 x 16)");
+    static_assert(NTT == 2 * NWV, "each wave stages two tiles");
+    constexpr int PBX = 16 * NTT;                        // picks per pass
     // the staged input of a 128-k group in MFMA fragment order: 1 KB block (tile tt, k step k) holds lane l's 16 bytes
     // (pick tt*16 + l%16, k 32k + 8(l/16)) at 16 l, written by one direct global-to-LDS load per block and read back
     // as one contiguous 1 KB wave read (no bank conflicts); two buffers, the next group loads while one computes
-    __shared__ __attribute__((aligned(16))) u32x4 xs0[32 * 64];
-    __shared__ __attribute__((aligned(16))) u32x4 xs1[32 * 64];
+    __shared__ __attribute__((aligned(16))) u32x4 xs0[NTT * 4 * 64];
+    __shared__ __attribute__((aligned(16))) u32x4 xs1[NTT * 4 * 64];
     Block rb;
-    if (DENSE) { rb.e = 0; rb.p0 = blockIdx.x * PB; rb.rows = min(PB, T - rb.p0); if (rb.rows <= 0) return; }
+    if (DENSE) { rb.e = 0; rb.p0 = blockIdx.x * PBX; rb.rows = min(PBX, T - rb.p0); if (rb.rows <= 0) return; }
     else if (!get_block(rbt, nrb, meta, n_tab, rb)) return;
-    // a block of more than PB picks runs as two halves, one after the other (the second reads the weights again,
-    // mostly from the caches); the barrier between them keeps the first half's last LDS reads ahead of the second
-    // half's first staging
-    for (int h0 = 0; h0 < rb.rows; h0 += PB)
+    // a block of more than PBX picks runs as passes of PBX, one after the other (a later pass reads the weights
+    // again, mostly from the caches); the barrier between them keeps one pass's last LDS reads ahead of the next
+    // pass's first staging
+    for (int h0 = 0; h0 < rb.rows; h0 += PBX)
     {
         if (h0) __syncthreads();
-        const Block b = {rb.e, rb.p0 + h0, min(PB, rb.rows - h0)};
+        const Block b = {rb.e, rb.p0 + h0, min(PBX, rb.rows - h0)};
         const int t = threadIdx.x, l = t & 63, row = l & 15;
         const int w = __builtin_amdgcn_readfirstlane(t >> 6);   // wave index, kept in a scalar register
-        const int nb0 = (blockIdx.y * 4 + w) * NS;
+        const int nb0 = (blockIdx.y * NWV + w) * NS;
         const uint8_t* wp[NMAT];
         const uint8_t* sp[NMAT];
         #pragma unroll
@@ -234,13 +238,13 @@ __global__ void __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(2))) pg
                     }
                 }
         };
-        f32x4 acc[NS][NMAT][8];
+        f32x4 acc[NS][NMAT][NTT];
         #pragma unroll
         for (int st = 0; st < NS; ++st)
             #pragma unroll
             for (int m = 0; m < NMAT; ++m)
                 #pragma unroll
-                for (int tt = 0; tt < 8; ++tt) acc[st][m][tt] = (f32x4) {0.f, 0.f, 0.f, 0.f};
+                for (int tt = 0; tt < NTT; ++tt) acc[st][m][tt] = (f32x4) {0.f, 0.f, 0.f, 0.f};
         stage(0, xs0);
         static_for<D>([&](auto sc) {
             fetch(decltype(sc)::value, sc);
@@ -279,11 +283,11 @@ __global__ void __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(2))) pg
                             a[st][m] = DENSE ? as_f16x8(ring[s].q[st][m][k]) : dq8s(ring[s].q[st][m][0][k], sh[st][m], dq);
                     // the k step's input tiles read together (tiles past the block read stale LDS data, never used), so
                     // the LDS latency is paid once per k step rather than once per tile
-                    f16x8 bvs[8];
+                    f16x8 bvs[NTT];
                     #pragma unroll
-                    for (int tt = 0; tt < 8; ++tt) bvs[tt] = as_f16x8(cur[(tt * 4 + k) * 64 + l]);
+                    for (int tt = 0; tt < NTT; ++tt) bvs[tt] = as_f16x8(cur[(tt * 4 + k) * 64 + l]);
                     #pragma unroll
-                    for (int tt = 0; tt < 8; ++tt)
+                    for (int tt = 0; tt < NTT; ++tt)
                     {
                         if (tt >= ntt) break;
                         #pragma unroll
@@ -297,7 +301,7 @@ __global__ void __launch_bounds__(PT) __attribute__((amdgpu_waves_per_eu(2))) pg
         }
         // epilogue: lane holds output rows 4(l/16)..+4 of pick tt*16 + l%16
         #pragma unroll
-        for (int tt = 0; tt < 8; ++tt)
+        for (int tt = 0; tt < NTT; ++tt)
         {
             const int pk = tt * 16 + row;
             if (pk >= b.rows) continue;
@@ -626,20 +630,19 @@ extern "C" int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid,
     }
     if (nrb > 0)
     {
-        pgemm_kernel<false, 2, 2, 3><<<dim3(nrb, I / 128), PT, 0, st>>>(xh, tok, wt, rbt, nrb, meta, n_tab, gw, uw, gs,
-                                                                             us, nullptr, nullptr, (_Float16*) ar,
-                                                                             nullptr, T, 0);
+        // 256-pick blocks in one pass: 8 waves, each one 16-row strip of gate and of up (or two of down) against the
+        // block's 16 pick tiles
+        pgemm_kernel<false, 2, 1, 4, EPI_ACT, 16, 8><<<dim3(nrb, I / 128), 512, 0, st>>>(
+            xh, tok, wt, rbt, nrb, meta, n_tab, gw, uw, gs, us, nullptr, nullptr, (_Float16*) ar, nullptr, T, 0);
         // (d held the f16 copy of x, which the gate/up GEMM has consumed by now: the down rows may overwrite it)
         if (inv)
-            pgemm_kernel<false, 1, 4, 2><<<dim3(nrb, H / 256), PT, 0, st>>>((const _Float16*) ar, nullptr, nullptr,
-                                                                                   rbt, nrb, meta, n_tab, dw, nullptr,
-                                                                                   ds, nullptr, nullptr, nullptr, nullptr,
-                                                                                   d, T, 0);
+            pgemm_kernel<false, 1, 2, 4, EPI_D, 16, 8><<<dim3(nrb, H / 256), 512, 0, st>>>(
+                (const _Float16*) ar, nullptr, nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, nullptr,
+                nullptr, d, T, 0);
         else
-            pgemm_kernel<false, 1, 4, 2, EPI_FIN><<<dim3(nrb, H / 256), PT, 0, st>>>((const _Float16*) ar, tok, nullptr,
-                                                                                    rbt, nrb, meta, n_tab, dw, nullptr,
-                                                                                    ds, nullptr, nullptr, nullptr,
-                                                                                    nullptr, nullptr, T, 0, out);
+            pgemm_kernel<false, 1, 2, 4, EPI_FIN, 16, 8><<<dim3(nrb, H / 256), 512, 0, st>>>(
+                (const _Float16*) ar, tok, nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, nullptr,
+                nullptr, nullptr, T, 0, out);
     }
     if (inv) pfin_kernel<<<T, 256, 0, st>>>(d, inv, topk, -1, out);
     return HMOE_LAUNCHED("moe4t_forward");
