@@ -25,9 +25,10 @@ constexpr int REC_E = 64;                   // record: word 0 = distinct experts
 
 // ---- error state of the C ABI (common.hip) ----
 int set_error(int code, const char* fmt, ...);
-// D[n][m] (row-major, leading dimension ldd, fp32) = X[n][k] . W[m][k]^T, f16 row-major operands (shared_gemm.hip)
-int lt_gemm(const _Float16* W, const _Float16* X, float* D, int m, int n, int k, int ldd, void* ws, size_t ws_bytes,
-            hipStream_t st);
+// the prefill shared expert (shared_gemm.hip), f16 row-major operands: act [T][I] = f16(silu(wg x) (wu x)), and
+// out [T][H] = wd act (fp32, written or, with add, added into)
+int dense_gate_up(const _Float16* wg, const _Float16* wu, const _Float16* x, int T, _Float16* act, hipStream_t st);
+int dense_down(const _Float16* wd, const _Float16* act, int T, float* out, bool add, hipStream_t st);
 int hip_check(hipError_t e, const char* what);
 #define HMOE_REQUIRE(cond, ...) do { if (!(cond)) return ::hmoe::set_error(HMOE_ERR_ARG, __VA_ARGS__); } while (0)
 #define HMOE_LAUNCHED(what) ::hmoe::hip_check(hipGetLastError(), what)

@@ -6,7 +6,7 @@
 // GEMMs: workgroup = (row block of <= 128 picks of one expert, 128 gate/up or 256 down output columns); see
 // pgemm_kernel. gu fuses act = silu(g) * u * w (f16), down writes d = W_d act (fp32), fin adds each
 // token's picks into out in top-k order (or with atomics, as p4_fin_kernel, when no inverse map is given). The shared
-// expert's projections run as library GEMMs (shared_gemm.hip) with sh_swiglu_kernel between them.
+// expert's projections run on the dense MFMA GEMMs of shared_gemm.hip.
 #include "hmoe_dev.h"
 
 namespace hmoe {
@@ -108,19 +108,16 @@ __device__ __forceinline__ bool get_block(const int* rbt, int nrb, const int* me
 // columns); wave w owns output strips nb0 = 4 NS blockIdx.y + NS w .. + NS (16 rows each) of NMAT matrices (gate and
 // up: NS = 2, or down: NS = 4), so every wave holds 4 weight fragments per k step and reads each 16-pick input
 // fragment from LDS once for 4 MFMAs. Per 128-k group kg:
-//   * the block's input rows are staged in LDS as f16 (double-buffered, one barrier per group); the next group's
-//     rows are loaded into registers while this group computes;
+//   * the block's input rows are staged in LDS as f16 by direct global-to-LDS loads (double-buffered, one barrier
+//     per group): the next group's rows load while this group computes;
 //   * the weight tiles come from a ring of D groups of unconditional 16-byte loads (and the lane's row scale), issued
 //     D groups ahead, so HBM latency hides behind D groups of MFMA work; each tile is loaded once per workgroup;
 //   * each k step dequantises the 4 weight fragments (exact f16 codes times the f16 group scale) and runs the
 //     16x16x32 MFMA against the block's 16-pick tiles (up to 8).
-// DENSE: a dense F16T matrix over every token (block b = tokens [128 b, 128 b + 128), weight 1; groups of 4 tiles).
-// hmoe_moe4p_forward runs the shared expert as library GEMMs instead (shared_gemm.hip: 0.17 against 0.32 ms per
-// 2048-token chunk on this kernel), so no launch here instantiates it; it is kept as the library-free form.
-template <bool DENSE, int NMAT, int NS>
+template <int NMAT, int NS>
 struct PFetch
 {
-    u32x4 q[NS][NMAT][DENSE ? 4 : 1];
+    u32x4 q[NS][NMAT];
     uint16_t s[NS][NMAT];
 };
 
@@ -130,31 +127,28 @@ enum { EPI_ACT = 0, EPI_RAW = 1, EPI_D = 2, EPI_FIN = 3 };
 
 // NTT: 16-pick tiles per pass (8: 128 picks, 4 waves; 16: 256 picks, 8 waves, one pass for the long prefill's 256-pick
 // blocks, each dequantised weight fragment feeding twice the MFMAs); NWV waves, each staging two tiles
-template <bool DENSE, int NMAT, int NS, int D, int EPI = NMAT == 2 ? EPI_ACT : EPI_D, int NTT = 8, int NWV = 4>
+template <int NMAT, int NS, int D, int EPI = NMAT == 2 ? EPI_ACT : EPI_D, int NTT = 8, int NWV = 4>
 __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) pgemm_kernel(
     const _Float16* __restrict__ xin, const int* __restrict__ tok, const float* __restrict__ wt,
     const int* __restrict__ rbt, int nrb, const int* __restrict__ meta, int n_tab,
     const int64_t* __restrict__ w0, const int64_t* __restrict__ w1, const int64_t* __restrict__ s0,
-    const int64_t* __restrict__ s1, const uint8_t* __restrict__ dense0, const uint8_t* __restrict__ dense1,
-    _Float16* __restrict__ ar, float* __restrict__ dout, int T, int off, float* __restrict__ fout = nullptr,
-    int ps = 0)
+    const int64_t* __restrict__ s1, _Float16* __restrict__ ar, float* __restrict__ dout, int T, int off,
+    float* __restrict__ fout = nullptr, int ps = 0)
 {
     static_assert((NMAT == 2) == (EPI == EPI_ACT || EPI == EPI_RAW), "gate/up epilogues need both matrices");
     constexpr int K = NMAT == 2 ? H : I;                 // gate/up: x [T][H] -> act; down: act [.][I] -> d
     constexpr int NOUT = NMAT == 2 ? I : H;
-    constexpr int KG = K / 128, KS = K / 32;
+    constexpr int KG = K / 128;
     static_assert(KG % D == 0, "the ring depth divides the k groups");
     static_assert(NS * NMAT * NTT == 32, "32 accumulator tiles per wave (4 fragments x 8 tiles or 2 x 16)");
     static_assert(NTT == 2 * NWV, "each wave stages two tiles");
     constexpr int PBX = 16 * NTT;                        // picks per pass
-    // the staged input of a 128-k group in MFMA fragment order: 1 KB block (tile tt, k step k) holds lane l's 16 bytes
-    // (pick tt*16 + l%16, k 32k + 8(l/16)) at 16 l, written by one direct global-to-LDS load per block and read back
-    // as one contiguous 1 KB wave read (no bank conflicts); two buffers, the next group loads while one computes
+    // the staged input of a 128-k group (four 1 KB blocks per 16-pick tile, below); two buffers, the next group loads
+    // while one computes
     __shared__ __attribute__((aligned(16))) u32x4 xs0[NTT * 4 * 64];
     __shared__ __attribute__((aligned(16))) u32x4 xs1[NTT * 4 * 64];
     Block rb;
-    if (DENSE) { rb.e = 0; rb.p0 = blockIdx.x * PBX; rb.rows = min(PBX, T - rb.p0); if (rb.rows <= 0) return; }
-    else if (!get_block(rbt, nrb, meta, n_tab, rb)) return;
+    if (!get_block(rbt, nrb, meta, n_tab, rb)) return;
     // a block of more than PBX picks runs as passes of PBX, one after the other (a later pass reads the weights
     // again, mostly from the caches); the barrier between them keeps one pass's last LDS reads ahead of the next
     // pass's first staging
@@ -170,34 +164,43 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
         #pragma unroll
         for (int m = 0; m < NMAT; ++m)
         {
-            wp[m] = DENSE ? (m == 0 ? dense0 : dense1) : (const uint8_t*) (m == 0 ? w0 : w1)[b.e];
-            sp[m] = DENSE ? nullptr : (const uint8_t*) (m == 0 ? s0 : s1)[b.e];
+            wp[m] = (const uint8_t*) (m == 0 ? w0 : w1)[b.e];
+            sp[m] = (const uint8_t*) (m == 0 ? s0 : s1)[b.e];
         }
         const int ntt = (b.rows + 15) >> 4;
         const DqConsts dq = dq_consts();
-        // wave w stages tiles 2w and 2w + 1: lane l's source row; a pick past the block re-reads a valid row (its output
-        // columns are never stored), a whole tile past the block reads one fixed 16 bytes
-        const _Float16* src[2];
+        // The staged input of a 128-k group: per 16-pick tile, four 1 KB blocks (k half kh, row half rh) of 8 rows x 64
+        // k; lane l of a block takes row l / 8's 16-byte chunk (l % 8) ^ (l / 8) (whole 128-byte lines from memory) and
+        // stores it at 16 l, so a fragment read (row l % 16, chunk 4 (k % 2) + l / 16 of k half k / 2) meets distinct
+        // banks. Wave w stages tiles 2w and 2w + 1: lane l's source row in each row half; a pick past the block re-reads
+        // a valid row (its output columns are never stored), a whole tile past the block reads one fixed 16 bytes.
+        const _Float16* src[2][2];
         #pragma unroll
         for (int h = 0; h < 2; ++h)
-        {
-            const int tt = 2 * w + h, pk = tt * 16 + row;
-            const bool in = pk < b.rows, tin = tt < ntt;
-            int srow;
-            if (NMAT == 2)
+            #pragma unroll
+            for (int rh = 0; rh < 2; ++rh)
             {
-                // (no token map: the picks' inputs are rows p0 .. of xin, as the moe4t test entry passes them)
-                const int tk = (DENSE || !tok) ? b.p0 + (in ? pk : 0) : tok[b.p0 + (in ? pk : 0)];
-                srow = (unsigned) tk < (unsigned) T ? tk : 0;
+                const int tt = 2 * w + h, pk = tt * 16 + 8 * rh + (l >> 3);
+                const bool in = pk < b.rows, tin = tt < ntt;
+                int srow;
+                if (NMAT == 2)
+                {
+                    // (no token map: the picks' inputs are rows p0 .. of xin, as the moe4t test entry passes them)
+                    const int tk = !tok ? b.p0 + (in ? pk : 0) : tok[b.p0 + (in ? pk : 0)];
+                    srow = (unsigned) tk < (unsigned) T ? tk : 0;
+                }
+                else srow = off + b.p0 + (in ? pk : 0);
+                src[h][rh] = xin + (size_t) srow * K + (tin ? 8 * ((l & 7) ^ (l >> 3)) : 0);
             }
-            else srow = off + b.p0 + (in ? pk : 0);
-            src[h] = xin + (size_t) srow * K + (tin ? 8 * (l >> 4) : 0);
-        }
+        int fo[4];
+        #pragma unroll
+        for (int k = 0; k < 4; ++k)
+            fo[k] = ((k >> 1) * 2 + (row >> 3)) * 64 + 8 * (l & 7) + ((4 * (k & 1) + (l >> 4)) ^ (l & 7));
         // Direct global-to-LDS loads (16 bytes per lane, lane l at LDS base + 16 l), issued from inline assembly: the
         // compiler then does not count them, so its own waits for the weight ring stay exact, and the wait that makes a
         // staged group visible is placed by hand before the barrier (the loads issued after a stage are exactly the
         // FETCH_LOADS of one ring refill). M0 holds the LDS base of each load; nothing else in this kernel uses M0.
-        constexpr int FETCH_LOADS = DENSE ? NS * NMAT * 4 : NS * NMAT * 2;
+        constexpr int FETCH_LOADS = NS * NMAT * 2;
         auto stage = [&](int kg, u32x4* buf) {
             #pragma unroll
             for (int h = 0; h < 2; ++h)
@@ -205,19 +208,21 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                 const int tt = 2 * w + h;
                 const bool tin = tt < ntt;
                 #pragma unroll
-                for (int k = 0; k < 4; ++k)
-                {
-                    const _Float16* gp = src[h] + (tin ? kg * 128 + 32 * k : 0);
-                    const uint32_t lds = __builtin_amdgcn_readfirstlane(
-                        (uint32_t) (uintptr_t) (__attribute__((address_space(3))) void*) (buf + (tt * 4 + k) * 64));
+                for (int kh = 0; kh < 2; ++kh)
+                    #pragma unroll
+                    for (int rh = 0; rh < 2; ++rh)
+                    {
+                        const _Float16* gp = src[h][rh] + (tin ? kg * 128 + 64 * kh : 0);
+                        const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t) (uintptr_t)
+                            (__attribute__((address_space(3))) void*) (buf + (tt * 4 + kh * 2 + rh) * 64));
     #pragma clang diagnostic push
     #pragma clang diagnostic ignored "-Winline-asm"
-                    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(gp), "s"(lds) : "memory", "m0");
+                        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(gp), "s"(lds) : "memory", "m0");
     #pragma clang diagnostic pop
-                }
+                    }
             }
         };
-        PFetch<DENSE, NMAT, NS> ring[D];
+        PFetch<NMAT, NS> ring[D];
         auto fetch = [&](int kg, auto sc) {
             constexpr int s = decltype(sc)::value;
             #pragma unroll
@@ -226,16 +231,8 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                 for (int m = 0; m < NMAT; ++m)
                 {
                     const int nb = nb0 + st;
-                    if (DENSE)
-                    {
-                        #pragma unroll
-                        for (int u = 0; u < 4; ++u) ring[s].q[st][m][u] = ldw16(wp[m] + ((size_t) (nb * KS + kg * 4 + u) * 64 + l) * 16);
-                    }
-                    else
-                    {
-                        ring[s].q[st][m][0] = ldw16(wp[m] + ((size_t) (nb * KG + kg) * 64 + l) * 16);
-                        ring[s].s[st][m] = ldg<uint16_t>(sp[m] + ((size_t) (nb * 16 + row) * KG + kg) * 2);
-                    }
+                    ring[s].q[st][m] = ldw16(wp[m] + ((size_t) (nb * KG + kg) * 64 + l) * 16);
+                    ring[s].s[st][m] = ldg<uint16_t>(sp[m] + ((size_t) (nb * 16 + row) * KG + kg) * 2);
                 }
         };
         f32x4 acc[NS][NMAT][NTT];
@@ -269,7 +266,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                     #pragma unroll
                     for (int m = 0; m < NMAT; ++m)
                     {
-                        const _Float16 h = DENSE ? (_Float16) 1.0f : (_Float16) bf2f(ring[s].s[st][m]);
+                        const _Float16 h = (_Float16) bf2f(ring[s].s[st][m]);
                         sh[st][m] = (f16x2) {h, h};
                     }
                 #pragma unroll
@@ -280,12 +277,12 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                     for (int st = 0; st < NS; ++st)
                         #pragma unroll
                         for (int m = 0; m < NMAT; ++m)
-                            a[st][m] = DENSE ? as_f16x8(ring[s].q[st][m][k]) : dq8s(ring[s].q[st][m][0][k], sh[st][m], dq);
+                            a[st][m] = dq8s(ring[s].q[st][m][k], sh[st][m], dq);
                     // the k step's input tiles read together (tiles past the block read stale LDS data, never used), so
                     // the LDS latency is paid once per k step rather than once per tile
                     f16x8 bvs[NTT];
                     #pragma unroll
-                    for (int tt = 0; tt < NTT; ++tt) bvs[tt] = as_f16x8(cur[(tt * 4 + k) * 64 + l]);
+                    for (int tt = 0; tt < NTT; ++tt) bvs[tt] = as_f16x8(cur[tt * 256 + fo[k]]);
                     #pragma unroll
                     for (int tt = 0; tt < NTT; ++tt)
                     {
@@ -317,7 +314,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                 }
                 else if (EPI == EPI_ACT)
                 {
-                    const float wv = DENSE ? 1.0f : wt[b.p0 + pk];
+                    const float wv = wt[b.p0 + pk];
                     _Float16 o[4];
                     #pragma unroll
                     for (int i = 0; i < 4; ++i) o[i] = (_Float16) (silu(acc[st][0][tt][i]) * acc[st][NMAT - 1][tt][i] * wv);
@@ -426,23 +423,8 @@ extern "C" int hmoe_dispatch(const int64_t* sel, const uint16_t* rw, int T, int 
 
 namespace hmoe {
 
-// the gu scratch: the f16 copy of x ([T][H], when xf = 0) at 0, the shared expert's gate | up sums (fp32 [T][2I])
-// at SH_C_OFF, the library GEMMs' workspace (SH_WS bytes) after them
-constexpr size_t SH_WS = 32u << 20;
-#define SH_C_OFF(T) (((size_t) (T) * H * 2 + 255) & ~(size_t) 255)
-
-// act[t] = f16(silu(g) u) of the shared expert's sums (the dense case of the grouped GEMM's epilogue)
-__global__ void __launch_bounds__(256) sh_swiglu_kernel(const float* __restrict__ gu, int T, _Float16* __restrict__ act)
-{
-    const size_t i = ((size_t) blockIdx.x * 256 + threadIdx.x) * 4;
-    if (i >= (size_t) T * I) return;
-    const size_t t = i / I, n = i - t * I;
-    const f32x4 g = *(const f32x4*) (gu + t * 2 * I + n), u = *(const f32x4*) (gu + t * 2 * I + I + n);
-    _Float16 o[4];
-    #pragma unroll
-    for (int k = 0; k < 4; ++k) o[k] = (_Float16) (silu(g[k]) * u[k]);
-    *(uint2*) (act + i) = *(const uint2*) o;
-}
+// the gu scratch: the f16 copy of x ([T][H], when xf = 0)
+#define SH_X_BYTES(T) (((size_t) (T) * H * 2 + 255) & ~(size_t) 255)
 
 }  // namespace hmoe
 
@@ -450,7 +432,7 @@ extern "C" size_t hmoe_moe4p_scratch_bytes(int which, int ps, int T)
 {
     switch (which)
     {
-        case 0: return SH_C_OFF(T) + (size_t) T * 2 * I * 4 + SH_WS;    // gu: x f16, shared g|u fp32, GEMM workspace
+        case 0: return SH_X_BYTES(T);                                   // gu: the f16 copy of x
         case 1: return (size_t) (ps + T) * I * 2;                       // ar f16 [ps + T][I]
         case 2: return (size_t) (ps + T) * H * 4;                       // d fp32 [ps + T][H]
         default: return 0;
@@ -471,8 +453,8 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
                  "moe4p_forward: npos %d nrb %d ps %d T %d topk %d", npos, nrb, ps, T, topk);
     HMOE_REQUIRE(n_tab >= 0 && n_tab <= HMOE_MAXE && (n_tab == 0 || (gw && uw && dw && gs && us && ds)),
                  "moe4p_forward: tables");
-    HMOE_REQUIRE((!sh_gw && !sh_uw && !sh_dw) || (sh_gw && sh_uw && sh_dw && inv && gu && ((uintptr_t) gu & 255) == 0),
-                 "moe4p_forward: the shared expert needs the inverse map and the gu scratch (256-byte aligned)");
+    HMOE_REQUIRE((!sh_gw && !sh_uw && !sh_dw) || (sh_gw && sh_uw && sh_dw && inv),
+                 "moe4p_forward: the shared expert needs all three matrices and the inverse map");
     HMOE_REQUIRE(((uintptr_t) x & 15) == 0 && ((uintptr_t) ar & 15) == 0 && ((uintptr_t) d & 15) == 0 &&
                  ((uintptr_t) out & 15) == 0, "moe4p_forward: alignment");
     HMOE_REQUIRE(xf == HMOE_XF_BF16 || xf == HMOE_XF_F16, "moe4p_forward: xf must be HMOE_XF_BF16 (0) or HMOE_XF_F16 "
@@ -490,38 +472,24 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
     // (inv given) or added into out[tok] by its epilogue (no inverse map: the atomic combine of p4_fin_kernel)
     if (nrb > 0)
     {
-        pgemm_kernel<false, 2, 2, 3><<<dim3(nrb, I / 128), PT, 0, st>>>((const _Float16*) xb, tok, wt, rbt, nrb, meta, n_tab, gw, uw,
-                                                                             gs, us, nullptr, nullptr, a, nullptr, T, 0);
+        pgemm_kernel<2, 2, 3><<<dim3(nrb, I / 128), PT, 0, st>>>((const _Float16*) xb, tok, wt, rbt, nrb, meta,
+            n_tab, gw, uw, gs, us, a, nullptr, T, 0);
         if (inv)
-            pgemm_kernel<false, 1, 4, 2><<<dim3(nrb, H / 256), PT, 0, st>>>(a, nullptr, nullptr, rbt,
-                                                                                   nrb, meta, n_tab, dw, nullptr, ds, nullptr,
-                                                                                   nullptr, nullptr, nullptr, d, T, 0);
+            pgemm_kernel<1, 4, 2><<<dim3(nrb, H / 256), PT, 0, st>>>(a, nullptr, nullptr, rbt, nrb, meta, n_tab, dw,
+                nullptr, ds, nullptr, nullptr, d, T, 0);
         else
-            pgemm_kernel<false, 1, 4, 2, EPI_FIN><<<dim3(nrb, H / 256), PT, 0, st>>>(a, tok, nullptr, rbt, nrb, meta, n_tab,
-                                                                                    dw, nullptr, ds, nullptr, nullptr,
-                                                                                    nullptr, nullptr, nullptr, T, 0, out);
+            pgemm_kernel<1, 4, 2, EPI_FIN><<<dim3(nrb, H / 256), PT, 0, st>>>(a, tok, nullptr, rbt, nrb, meta, n_tab,
+                dw, nullptr, ds, nullptr, nullptr, nullptr, T, 0, out);
     }
     const bool sh = sh_gw != nullptr;
     if (sh)
     {
-        // the shared expert on every token: gate and up as library GEMMs into the fp32 sums [T][2I] of the gu scratch,
-        // act rows ps.. = f16(silu(g) u), then down into d rows ps.. (fp32) for the combine
-        uint8_t* scr = (uint8_t*) gu;
-        float* c = (float*) (scr + SH_C_OFF(T));
-        void* ws = scr + SH_C_OFF(T) + (size_t) T * 2 * I * 4;
-        const _Float16* xs = (const _Float16*) xb;
-        // (gate and up in one GEMM of 2I rows when up follows gate in memory)
-        if ((const _Float16*) sh_uw == (const _Float16*) sh_gw + (size_t) I * H)
-        {
-            if (int rc = lt_gemm((const _Float16*) sh_gw, xs, c, 2 * I, T, H, 2 * I, ws, SH_WS, st)) return rc;
-        }
-        else
-        {
-            if (int rc = lt_gemm((const _Float16*) sh_gw, xs, c, I, T, H, 2 * I, ws, SH_WS, st)) return rc;
-            if (int rc = lt_gemm((const _Float16*) sh_uw, xs, c + I, I, T, H, 2 * I, ws, SH_WS, st)) return rc;
-        }
-        sh_swiglu_kernel<<<(unsigned) (((size_t) T * I / 4 + 255) / 256), 256, 0, st>>>(c, T, a + (size_t) ps * I);
-        if (int rc = lt_gemm((const _Float16*) sh_dw, a + (size_t) ps * I, d + (size_t) ps * H, H, T, I, H, ws, SH_WS, st))
+        // the shared expert on every token: act rows ps.. = f16(silu(gate x) up x), then down into d rows ps.. (fp32),
+        // which the ordered combine adds after each token's picks
+        if (int rc = dense_gate_up((const _Float16*) sh_gw, (const _Float16*) sh_uw, (const _Float16*) xb, T,
+                                   a + (size_t) ps * I, st))
+            return rc;
+        if (int rc = dense_down((const _Float16*) sh_dw, a + (size_t) ps * I, T, d + (size_t) ps * H, false, st))
             return rc;
     }
     if (inv) pfin_kernel<<<T, 256, 0, st>>>(d, inv, topk, sh ? ps : -1, out);
@@ -534,23 +502,13 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
 // ---------------------------------------------------------------------------------------------------------------
 namespace hmoe {
 
-// out[t] += d[t] (each element has one writer: deterministic)
-__global__ void __launch_bounds__(256) add_rows_kernel(const float* __restrict__ d, size_t n, float* __restrict__ out)
-{
-    for (size_t i = (blockIdx.x * (size_t) 256 + threadIdx.x) * 4; i < n; i += (size_t) gridDim.x * 256 * 4)
-        *(f32x4*) (out + i) = *(const f32x4*) (out + i) + *(const f32x4*) (d + i);
-}
-
-// work layout: x f16 copy [T][H] | g|u fp32 [T][2I] | act f16 [T][I] | d fp32 [T][H] | library workspace
-static size_t shw_x(int T) { return 0; }
-static size_t shw_gu(int T) { return ((size_t) T * H * 2 + 255) & ~(size_t) 255; }
-static size_t shw_act(int T) { return shw_gu(T) + (size_t) T * 2 * I * 4; }
-static size_t shw_d(int T) { return shw_act(T) + (((size_t) T * I * 2 + 255) & ~(size_t) 255); }
-static size_t shw_ws(int T) { return shw_d(T) + (size_t) T * H * 4; }
+// work layout: x f16 copy [T][H] | act f16 [T][I]
+static size_t shw_act(int T) { return SH_X_BYTES(T); }
+static size_t shw_end(int T) { return shw_act(T) + (((size_t) T * I * 2 + 255) & ~(size_t) 255); }
 
 }  // namespace hmoe
 
-extern "C" size_t hmoe_shared_work_bytes(int T) { return shw_ws(T > 0 ? T : 1) + SH_WS; }
+extern "C" size_t hmoe_shared_work_bytes(int T) { return shw_end(T > 0 ? T : 1); }
 
 extern "C" int hmoe_shared_forward(const void* x, int T, const void* sh_gw, const void* sh_uw, const void* sh_dw,
                                    void* work, float* out, int xf, void* stream)
@@ -565,25 +523,13 @@ extern "C" int hmoe_shared_forward(const void* x, int T, const void* sh_gw, cons
     const _Float16* xs = (const _Float16*) x;
     if (xf == HMOE_XF_BF16)
     {
-        to_f16_kernel<<<1024, 256, 0, st>>>((const uint16_t*) x, (size_t) T * H, (_Float16*) (wk + shw_x(T)));
-        xs = (const _Float16*) (wk + shw_x(T));
+        to_f16_kernel<<<1024, 256, 0, st>>>((const uint16_t*) x, (size_t) T * H, (_Float16*) wk);
+        xs = (const _Float16*) wk;
     }
-    float* c = (float*) (wk + shw_gu(T));
     _Float16* a = (_Float16*) (wk + shw_act(T));
-    float* d = (float*) (wk + shw_d(T));
-    void* ws = wk + shw_ws(T);
-    if ((const _Float16*) sh_uw == (const _Float16*) sh_gw + (size_t) I * H)
-    {
-        if (int rc = lt_gemm((const _Float16*) sh_gw, xs, c, 2 * I, T, H, 2 * I, ws, SH_WS, st)) return rc;
-    }
-    else
-    {
-        if (int rc = lt_gemm((const _Float16*) sh_gw, xs, c, I, T, H, 2 * I, ws, SH_WS, st)) return rc;
-        if (int rc = lt_gemm((const _Float16*) sh_uw, xs, c + I, I, T, H, 2 * I, ws, SH_WS, st)) return rc;
-    }
-    sh_swiglu_kernel<<<(unsigned) (((size_t) T * I / 4 + 255) / 256), 256, 0, st>>>(c, T, a);
-    if (int rc = lt_gemm((const _Float16*) sh_dw, a, d, H, T, I, H, ws, SH_WS, st)) return rc;
-    add_rows_kernel<<<1024, 256, 0, st>>>(d, (size_t) T * H, out);
+    if (int rc = dense_gate_up((const _Float16*) sh_gw, (const _Float16*) sh_uw, xs, T, a, st)) return rc;
+    // (out += each product element once, in the GEMM's epilogue)
+    if (int rc = dense_down((const _Float16*) sh_dw, a, T, out, true, st)) return rc;
     return HMOE_LAUNCHED("shared_forward");
 }
 
@@ -632,17 +578,15 @@ extern "C" int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid,
     {
         // 256-pick blocks in one pass: 8 waves, each one 16-row strip of gate and of up (or two of down) against the
         // block's 16 pick tiles
-        pgemm_kernel<false, 2, 1, 4, EPI_ACT, 16, 8><<<dim3(nrb, I / 128), 512, 0, st>>>(
-            xh, tok, wt, rbt, nrb, meta, n_tab, gw, uw, gs, us, nullptr, nullptr, (_Float16*) ar, nullptr, T, 0);
+        pgemm_kernel<2, 1, 4, EPI_ACT, 16, 8><<<dim3(nrb, I / 128), 512, 0, st>>>(xh, tok, wt, rbt, nrb, meta, n_tab,
+            gw, uw, gs, us, (_Float16*) ar, nullptr, T, 0);
         // (d held the f16 copy of x, which the gate/up GEMM has consumed by now: the down rows may overwrite it)
         if (inv)
-            pgemm_kernel<false, 1, 2, 4, EPI_D, 16, 8><<<dim3(nrb, H / 256), 512, 0, st>>>(
-                (const _Float16*) ar, nullptr, nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, nullptr,
-                nullptr, d, T, 0);
+            pgemm_kernel<1, 2, 4, EPI_D, 16, 8><<<dim3(nrb, H / 256), 512, 0, st>>>((const _Float16*) ar, nullptr,
+                nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, d, T, 0);
         else
-            pgemm_kernel<false, 1, 2, 4, EPI_FIN, 16, 8><<<dim3(nrb, H / 256), 512, 0, st>>>(
-                (const _Float16*) ar, tok, nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, nullptr,
-                nullptr, nullptr, T, 0, out);
+            pgemm_kernel<1, 2, 4, EPI_FIN, 16, 8><<<dim3(nrb, H / 256), 512, 0, st>>>((const _Float16*) ar, tok,
+                nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, nullptr, T, 0, out);
     }
     if (inv) pfin_kernel<<<T, 256, 0, st>>>(d, inv, topk, -1, out);
     return HMOE_LAUNCHED("moe4t_forward");
@@ -659,14 +603,10 @@ extern "C" int hmoe_moe4t_gemm(const void* xs, int rows, const int* rbt, int nrb
     if (nrb == 0) return HMOE_OK;
     hipStream_t st = (hipStream_t) stream;
     if (down)
-        pgemm_kernel<false, 1, 4, 2><<<dim3(nrb, H / 256), PT, 0, st>>>((const _Float16*) xs, nullptr, nullptr, rbt,
-                                                                               nrb, nullptr, n_tab, w0, nullptr, s0,
-                                                                               nullptr, nullptr, nullptr, nullptr, out,
-                                                                               rows, 0);
+        pgemm_kernel<1, 4, 2><<<dim3(nrb, H / 256), PT, 0, st>>>((const _Float16*) xs, nullptr, nullptr, rbt, nrb,
+            nullptr, n_tab, w0, nullptr, s0, nullptr, nullptr, out, rows, 0);
     else
-        pgemm_kernel<false, 2, 2, 3, EPI_RAW><<<dim3(nrb, I / 128), PT, 0, st>>>((const _Float16*) xs, nullptr, nullptr,
-                                                                                rbt, nrb, nullptr, n_tab, w0, w1, s0,
-                                                                                s1, nullptr, nullptr, nullptr, out,
-                                                                                rows, 0, nullptr, ps);
+        pgemm_kernel<2, 2, 3, EPI_RAW><<<dim3(nrb, I / 128), PT, 0, st>>>((const _Float16*) xs, nullptr, nullptr,
+            rbt, nrb, nullptr, n_tab, w0, w1, s0, s1, nullptr, out, rows, 0, nullptr, ps);
     return HMOE_LAUNCHED("moe4t_gemm");
 }

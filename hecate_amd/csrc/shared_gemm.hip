@@ -1,102 +1,183 @@
-// shared_gemm.hip - the prefill shared expert's two projections as plain library GEMMs (hipBLASLt: f16 operands,
-// fp32 accumulation and output). The shared expert is a dense bf16 MLP (its weights are exact in f16), so it needs no
-// dequantisation and a library GEMM runs it near the MFMA peak. The reference keeps the shared expert outside its
-// routed op as well (runtime/tier/tier_split.py:548-560: at decode into the accumulator, at prefill through the model's
-// own shared-expert forward). The routed int4 experts stay on the hand-written grouped GEMM.
+// shared_gemm.hip - the prefill shared expert's projections as hand-written dense MFMA GEMMs (f16 operands, fp32
+// accumulation). The shared expert is a dense bf16 MLP (its weights are exact in f16), run over every token of the
+// chunk; the reference keeps it outside its routed op at prefill (runtime/tier/tier_split.py:548-560, the model's own
+// shared-expert forward). gate and up run as one GEMM whose epilogue writes act = f16(silu(g) u); down writes fp32
+// rows (the ordered combine adds them) or adds them into out.
 //
-// lt_gemm: D[n][m] (row-major, leading dimension ldd) = X[n][k] . W[m][k]^T. In hipBLASLt's column-major terms that is
-// D^T (m x n, ld ldd) = op(A) B with A = W seen as k x m (ld k, op = transpose) and B = X seen as k x n (ld k).
-// One library handle per device and one plan (descriptors + the heuristic's algorithm) per shape, made on first use
-// under a mutex and kept for the process; after that a call only queues the GEMM on the stream.
+// dgemm_kernel: D[n][m] = sum_k X[n][k] W[m][k] over row-major W [M][K] (one matrix, or gate and up as two) and X
+// [N][K]. Workgroup = 4 waves as 2 (m) x 2 (n) = 32 TM / NMAT output rows x 32 TN tokens; wave (wm, wn) holds TM
+// weight tiles (TM / NMAT of each matrix) x TN token tiles of 16 x 16 in its accumulators. K runs in stages of 64:
+// both operands of a stage go to LDS by direct global-to-LDS loads, in a ring of 3 stages issued two ahead, so the
+// one wait and barrier per stage find the stage long arrived. A stage holds each 8 rows' 128 bytes as a 1 KB block:
+// one load per block, lane l taking row l / 8's 16-byte chunk (l % 8) ^ (l / 8) (whole 128-byte lines from memory),
+// stored at 16 l; the swizzle puts the 16 rows x 16 bytes of an MFMA fragment read (row l % 16, chunk 4 ks + l / 16)
+// on distinct banks. Each 32-k step reads the wave's TM + TN fragments and runs TM TN MFMAs. A token past N reads
+// row N - 1 and is not stored.
 #include "hmoe_dev.h"
-
-#include <hipblaslt/hipblaslt.h>
-
-#include <map>
-#include <mutex>
-#include <tuple>
 
 namespace hmoe {
 
-namespace {
+enum { DG_ACT = 0, DG_D = 1, DG_ADD = 2 };
 
-struct LtPlan
+template <int NMAT, int TM, int TN, int EPI>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) dgemm_kernel(
+    const _Float16* __restrict__ w0, const _Float16* __restrict__ w1, const _Float16* __restrict__ x, int N, int K,
+    void* __restrict__ out, int ldo)
 {
-    hipblasLtMatmulDesc_t desc = nullptr;
-    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
-    hipblasLtMatmulAlgo_t algo{};
-};
-
-std::mutex g_lt_mu;
-hipblasLtHandle_t g_lt[64] = {};
-std::map<std::tuple<int, int, int, int, int, size_t>, LtPlan> g_plans;   // (device, m, n, k, ldd, workspace)
-
-int lt_fail(const char* what, hipblasStatus_t s)
-{
-    return set_error(HMOE_ERR_HIP, "shared expert GEMM: %s failed (hipBLASLt status %d)", what, (int) s);
-}
-
-#define LT_TRY(call)                                             \
-    do {                                                         \
-        const hipblasStatus_t s_ = (call);                       \
-        if (s_ != HIPBLAS_STATUS_SUCCESS) return lt_fail(#call, s_); \
-    } while (0)
-
-int make_plan(hipblasLtHandle_t h, int m, int n, int k, int ldd, size_t ws_bytes, LtPlan& p)
-{
-    LT_TRY(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F));
-    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-    LT_TRY(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)));
-    LT_TRY(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)));
-    LT_TRY(hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16F, k, m, k));
-    LT_TRY(hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16F, k, n, k));
-    LT_TRY(hipblasLtMatrixLayoutCreate(&p.c, HIP_R_32F, m, n, ldd));
-    hipblasLtMatmulPreference_t pref = nullptr;
-    LT_TRY(hipblasLtMatmulPreferenceCreate(&pref));
-    const uint64_t wsb = ws_bytes;
-    hipblasStatus_t s = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
-                                                              sizeof(wsb));
-    hipblasLtMatmulHeuristicResult_t res{};
-    int found = 0;
-    if (s == HIPBLAS_STATUS_SUCCESS)
-        s = hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.a, p.b, p.c, p.c, pref, 1, &res, &found);
-    hipblasLtMatmulPreferenceDestroy(pref);
-    if (s != HIPBLAS_STATUS_SUCCESS) return lt_fail("hipblasLtMatmulAlgoGetHeuristic", s);
-    if (found < 1 || res.workspaceSize > ws_bytes)
-        return set_error(HMOE_ERR_HIP, "shared expert GEMM: no algorithm for m %d n %d k %d within %zu workspace bytes",
-                         m, n, k, ws_bytes);
-    p.algo = res.algo;
-    return HMOE_OK;
-}
-
-}  // namespace
-
-int lt_gemm(const _Float16* W, const _Float16* X, float* D, int m, int n, int k, int ldd, void* ws, size_t ws_bytes,
-            hipStream_t st)
-{
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
-        return set_error(HMOE_ERR_HIP, "shared expert GEMM: current device");
-    const LtPlan* plan = nullptr;
-    hipblasLtHandle_t h = nullptr;
+    static_assert((NMAT == 2) == (EPI == DG_ACT), "the SwiGLU epilogue pairs gate and up");
+    constexpr int NST = 3;                              // LDS stages, issued NST - 1 ahead
+    constexpr int TMO = TM / NMAT;                      // tiles per matrix per wave
+    constexpr int AT = 2 * TM, BT = 2 * TN;             // weight and token tiles of the workgroup
+    constexpr int NB = (AT + BT) * 2;                   // 1 KB blocks (8 rows x 64 k) per stage
+    constexpr int SL = NB / 4;                          // blocks staged per wave per stage
+    static_assert(NB % 4 == 0 && TM % NMAT == 0 && TM * TN <= 64, "4 waves share the staging; 256 accumulators");
+    __shared__ __attribute__((aligned(16))) u32x4 lds[NST][NB * 64];
+    const int t = threadIdx.x, l = t & 63, row = l & 15;
+    const int w = __builtin_amdgcn_readfirstlane(t >> 6), wm = w & 1, wn = w >> 1;
+    const int m0 = blockIdx.x * 2 * 16 * TMO;           // first output row of each matrix
+    const int n0 = blockIdx.y * 2 * 16 * TN;            // first token
+    const int KS = K / 64;
+    // the blocks this wave stages (b = w + 4 i): block b holds rows 8 b .. + 8 of the stage's tiles (weight tiles
+    // first: tile a = matrix a / (2 TMO), rows 16 (a % (2 TMO)) .., then token tiles); a scalar base per block and the
+    // lane's byte offset from it
+    const _Float16* sb[SL];
+    uint32_t vo[SL];
+    const uint32_t chunk = 16u * (uint32_t) ((l & 7) ^ (l >> 3));
+    #pragma unroll
+    for (int i = 0; i < SL; ++i)
     {
-        std::lock_guard<std::mutex> lock(g_lt_mu);
-        if (!g_lt[dev]) LT_TRY(hipblasLtCreate(&g_lt[dev]));
-        h = g_lt[dev];
-        const auto key = std::make_tuple(dev, m, n, k, ldd, ws_bytes);
-        auto it = g_plans.find(key);
-        if (it == g_plans.end())
+        const int b = w + 4 * i, tile = b >> 1, r = 8 * (b & 1) + (l >> 3);
+        if (tile < AT)
         {
-            LtPlan p;
-            if (int rc = make_plan(h, m, n, k, ldd, ws_bytes, p)) return rc;
-            it = g_plans.emplace(key, p).first;
+            const int mat = tile / (2 * TMO), tr = tile % (2 * TMO);
+            sb[i] = (mat == 0 ? w0 : w1) + (size_t) (m0 + 16 * tr) * K;
+            vo[i] = (uint32_t) r * (K * 2) + chunk;
         }
-        plan = &it->second;                                      // (map nodes do not move)
+        else
+        {
+            const int tk = min(n0 + 16 * (tile - AT) + r, N - 1);
+            sb[i] = x;
+            vo[i] = (uint32_t) tk * (K * 2) + chunk;
+        }
     }
-    const float alpha = 1.0f, beta = 0.0f;
-    LT_TRY(hipblasLtMatmul(h, plan->desc, &alpha, W, plan->a, X, plan->b, &beta, D, plan->c, D, plan->c, &plan->algo,
-                           ws, ws_bytes, st));
-    return HMOE_OK;
+    // stage s into LDS buffer s % NST; a stage past the last (kept so every stage issues the same loads, which the
+    // wait counts) reads one fixed 16 bytes
+    auto stage = [&](int s) {
+        const bool live = s < KS;
+        u32x4* buf = lds[s % NST];
+        #pragma unroll
+        for (int i = 0; i < SL; ++i)
+        {
+            const _Float16* base = sb[i] + (live ? 64 * s : 0);
+            const uint32_t v = live ? vo[i] : 0u;
+            const uint32_t la = __builtin_amdgcn_readfirstlane(
+                (uint32_t) (uintptr_t) (__attribute__((address_space(3))) void*) (buf + (w + 4 * i) * 64));
+    #pragma clang diagnostic push
+    #pragma clang diagnostic ignored "-Winline-asm"
+            asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" :: "v"(v), "s"(base), "s"(la)
+                         : "memory", "m0");
+    #pragma clang diagnostic pop
+        }
+    };
+    // a fragment's lane l: row l % 16 of the tile (block 2 tile + (l % 16) / 8, row (l % 8) in it), chunk 4 ks + l / 16
+    int fo[2];
+    #pragma unroll
+    for (int ks = 0; ks < 2; ++ks) fo[ks] = 64 * (row >> 3) + 8 * (l & 7) + (((4 * ks + (l >> 4)) ^ (l & 7)));
+    f32x4 acc[TM][TN];
+    #pragma unroll
+    for (int i = 0; i < TM; ++i)
+        #pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = (f32x4) {0.f, 0.f, 0.f, 0.f};
+    #pragma unroll
+    for (int s = 0; s < NST - 1; ++s) stage(s);
+    for (int s = 0; s < KS; ++s)
+    {
+        // stage s is complete when at most the NST - 2 later stages' loads are outstanding
+        asm volatile("s_waitcnt vmcnt(%0)" :: "n"((NST - 2) * SL) : "memory");
+        __syncthreads();
+        const u32x4* cur = lds[s % NST];
+        // both 32-k steps' fragments are read first (in issue order, so the first step's MFMAs wait only for their
+        // own reads), then the first step's MFMAs, the next stage's loads (issued while those MFMAs run) and the second
+        // step's MFMAs: one LDS latency per stage
+        f16x8 a[2][TM], bv[2][TN];
+        #pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+        {
+            #pragma unroll
+            for (int i = 0; i < TM; ++i)
+            {
+                const int tile = (i / TMO) * 2 * TMO + wm * TMO + i % TMO;
+                a[ks][i] = as_f16x8(cur[tile * 128 + fo[ks]]);
+            }
+            #pragma unroll
+            for (int j = 0; j < TN; ++j) bv[ks][j] = as_f16x8(cur[(AT + wn * TN + j) * 128 + fo[ks]]);
+        }
+        #pragma unroll
+        for (int i = 0; i < TM; ++i)
+            #pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = mfma16(a[0][i], bv[0][j], acc[i][j]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * (TM + TN), 0);   // the LDS reads
+        __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);         // then the first step's MFMAs
+        stage(s + NST - 1);
+        #pragma unroll
+        for (int i = 0; i < TM; ++i)
+            #pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = mfma16(a[1][i], bv[1][j], acc[i][j]);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // lane l holds output rows 4 (l / 16) .. + 4 of each weight tile for token 16 j + l % 16 of its token tiles
+    #pragma unroll
+    for (int j = 0; j < TN; ++j)
+    {
+        const int n = n0 + 16 * (wn * TN + j) + row;
+        if (n >= N) continue;
+        #pragma unroll
+        for (int i = 0; i < TMO; ++i)
+        {
+            const int m = m0 + 16 * (wm * TMO + i) + 4 * (l >> 4);
+            if (EPI == DG_ACT)
+            {
+                _Float16 o[4];
+                #pragma unroll
+                for (int q = 0; q < 4; ++q) o[q] = (_Float16) (silu(acc[i][j][q]) * acc[TMO + i][j][q]);
+                *(uint2*) ((_Float16*) out + (size_t) n * ldo + m) = *(const uint2*) o;
+            }
+            else
+            {
+                f32x4* o = (f32x4*) ((float*) out + (size_t) n * ldo + m);
+                *o = EPI == DG_ADD ? *o + acc[i][j] : acc[i][j];
+            }
+        }
+    }
 }
+
+// gate and up: workgroups of 128 act columns x 128 tokens (TM 8 = 4 gate + 4 up tiles, TN 4: I / 128 x T / 128, 256
+// workgroups at 2048 tokens, one per CU); down: 192 output rows x 128 tokens (TM 6, TN 4: 512 workgroups at 2048)
+constexpr int GU_TM = 8, GU_TN = 4;
+constexpr int DN_TM = 6, DN_TN = 4;
 
 }  // namespace hmoe
+
+using namespace hmoe;
+
+int hmoe::dense_gate_up(const _Float16* wg, const _Float16* wu, const _Float16* x, int T, _Float16* act, hipStream_t st)
+{
+    constexpr int BM = 32 * GU_TM / 2, BN = 32 * GU_TN;
+    static_assert(I % BM == 0 && H % 64 == 0, "gate/up tiling");
+    HMOE_REQUIRE(T >= 1 && ((uintptr_t) wg & 15) == 0 && ((uintptr_t) wu & 15) == 0 && ((uintptr_t) x & 15) == 0 &&
+                 ((uintptr_t) act & 7) == 0, "shared gate/up: T %d or alignment", T);
+    dgemm_kernel<2, GU_TM, GU_TN, DG_ACT><<<dim3(I / BM, (T + BN - 1) / BN), 256, 0, st>>>(wg, wu, x, T, H, act, I);
+    return HMOE_LAUNCHED("shared gate/up");
+}
+
+int hmoe::dense_down(const _Float16* wd, const _Float16* act, int T, float* out, bool add, hipStream_t st)
+{
+    constexpr int BM = 32 * DN_TM, BN = 32 * DN_TN;
+    static_assert(H % BM == 0 && I % 64 == 0, "down tiling");
+    HMOE_REQUIRE(T >= 1 && ((uintptr_t) wd & 15) == 0 && ((uintptr_t) act & 15) == 0 && ((uintptr_t) out & 15) == 0,
+                 "shared down: T %d or alignment", T);
+    const dim3 g(H / BM, (T + BN - 1) / BN);
+    if (add) dgemm_kernel<1, DN_TM, DN_TN, DG_ADD><<<g, 256, 0, st>>>(wd, nullptr, act, T, I, out, H);
+    else dgemm_kernel<1, DN_TM, DN_TN, DG_D><<<g, 256, 0, st>>>(wd, nullptr, act, T, I, out, H);
+    return HMOE_LAUNCHED("shared down");
+}

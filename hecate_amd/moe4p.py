@@ -13,7 +13,7 @@ H, I = 6144, 2048
 
 def scratch(dev, npos, T=0):
     """moe4p.cu:209-215: [gu, ar, d] for up to npos picks (+ T rows for the shared expert); gu holds the f16 copy of
-    x when forward gets bf16 x, then (with the shared expert) its fp32 gate | up sums and the library GEMMs' workspace"""
+    x when forward gets bf16 x"""
     dev = torch.device(dev)
     L = lib()
     return [torch.zeros(int(L.hmoe_moe4p_scratch_bytes(0, npos, T)) // 4, dtype=torch.float32, device=dev),
@@ -41,8 +41,8 @@ def forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, inv=No
     if npos > ps or d.shape[0] < ar.shape[0]:
         raise RuntimeError(f"moe4p: scratch holds {ps} picks, {npos} given")
     # the scratch at least as large as the library writes it (a short one would be written past its end): gu holds
-    # the f16 copy of x when x is bf16, and the shared expert's sums and GEMM workspace when it is given
-    need = int(lib().hmoe_moe4p_scratch_bytes(0, ps, T)) if shared is not None else (T * H * 2 if xf == XF_BF16 else 0)
+    # the f16 copy of x when x is bf16
+    need = int(lib().hmoe_moe4p_scratch_bytes(0, ps, T)) if xf == XF_BF16 else 0
     if need and (gu is None or gu.numel() * gu.element_size() < need):
         raise RuntimeError(f"moe4p: the gu scratch needs {need} bytes")
     if ar.dim() != 2 or ar.shape[1] != I or d.dim() != 2 or d.shape[1] != H:

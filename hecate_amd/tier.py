@@ -256,9 +256,8 @@ class MoELayer:
                       inv=pf.inv[:T * self.topk], meta=pf.meta, topk=self.topk, shared=sh, npos=pf.F, nrb=pf.nrb_max)
 
     def shared_rows(self):
-        """the shared expert as row-major f16 (gate [I, H], up [I, H], down [H, I]) for the prefill's library GEMMs,
-        made from the F16T copies on first use; gate and up are the two halves of one [2I, H] matrix, so that the
-        library runs them as one GEMM"""
+        """the shared expert as row-major f16 (gate [I, H], up [I, H], down [H, I]) for the prefill's dense GEMMs,
+        made from the F16T copies on first use"""
         if self._shared_rows is None:
             g, u, d = self.shared
             gu = torch.cat([f16t_rows(g, I, H), f16t_rows(u, I, H)])

@@ -166,15 +166,13 @@ int hmoe_dispatch(const int64_t* sel, const uint16_t* rw, int T, int topk, int l
  * rbt), wt fp32 [npos]; rbt int32 [nrb][4] rows {expert (relative to the tables), first pick, picks <= 256, 0} (a
  * block of more than 128 picks runs as two halves in one workgroup; the dispatch's bm is at most 256);
  * tables (n_tab entries) as in hmoe_moe4_forward; ar f16 [ps + T][I] and d fp32 [ps + T][H] scratch
- * (hmoe_moe4p_scratch_bytes); gu (256-byte aligned, hmoe_moe4p_scratch_bytes(0) bytes): the f16 copy of x [T][H]
- * when x is bf16, then with the shared expert its fp32 gate | up sums [T][2I] and the library GEMMs' workspace (NULL
- * allowed for fp16 x without the shared expert); out fp32 [T][H] accumulated into. meta: NULL, or the device
+ * (hmoe_moe4p_scratch_bytes); gu (16-byte aligned, hmoe_moe4p_scratch_bytes(0) bytes): the f16 copy of x [T][H]
+ * when x is bf16 (NULL allowed for fp16 x); out fp32 [T][H] accumulated into. meta: NULL, or the device
  * {npos, nrb} written by hmoe_dispatch (then npos / nrb are the static maxima the grids are sized for). inv: NULL
  * (picks added with atomics, as p4_fin_kernel) or the dispatch's inverse map (each token's picks added in top-k
  * order: deterministic). sh_*: the shared expert as row-major f16 (gate [I][H], up [I][H], down [H][I]) or NULL
- * (needs inv and gu); it runs on every token with weight 1, its projections as library GEMMs (hipBLASLt, fp32
- * accumulation; a plan per token count is made on the first call with that count, so capture a graph after one eager
- * call). T = 0 with npos = 0 is a no-op. */
+ * (needs inv); it runs on every token with weight 1 on dense MFMA GEMMs (fp32 accumulation; act rows ps.. and d
+ * rows ps.. hold its SwiGLU and down output, added after each token's picks). T = 0 with npos = 0 is a no-op. */
 size_t hmoe_moe4p_scratch_bytes(int which, int ps, int T);     /* which: 0 gu, 1 ar, 2 d */
 int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid, const float* wt, const int* rbt, int npos,
                        int nrb, int n_tab, const int64_t* gw, const int64_t* uw, const int64_t* dw, const int64_t* gs,
@@ -210,7 +208,8 @@ int hmoe_moe4t_gemm(const void* xs, int rows, const int* rbt, int nrb, int n_tab
 /* ---- the shared expert alone over a chunk (this build's addition: the reference runs it through the model's own
  * shared-expert MLP at prefill, runtime/tier/tier_split.py:548-560, next to moe4t): out fp32 [T][H] += down(silu(gate
  * x) * up x), x bf16 / fp16 [T][H] (xf as above), the weights row-major f16 (gate [I][H], up [I][H], down [H][I]);
- * work: hmoe_shared_work_bytes(T) bytes, 256-byte aligned. Every output element is added once: deterministic. */
+ * work: hmoe_shared_work_bytes(T) bytes, 256-byte aligned (the f16 copy of x, act f16 [T][I]). Every output
+ * element is added once, by the down GEMM's epilogue: deterministic. */
 size_t hmoe_shared_work_bytes(int T);
 int hmoe_shared_forward(const void* x, int T, const void* sh_gw, const void* sh_uw, const void* sh_dw, void* work,
                         float* out, int xf, void* stream);

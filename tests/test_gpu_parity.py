@@ -465,14 +465,14 @@ def test_host_tensors_are_refused(dev):
 
 
 def test_prefill_replays_in_a_graph(dev):
-    """a prefill chunk (router, device dispatch plan, grouped GEMMs, the shared expert's library GEMMs, combine, bf16
+    """a prefill chunk (router, device dispatch plan, grouped GEMMs, the shared expert's dense GEMMs, combine, bf16
     out) captured once and replayed, with eager work and synchronisations between replays: every replay gives the
     eager chunk's bits"""
     log("prefill graph T=300")
     lay = gpu_layer("c2", dev, layer=0, bias_sigma=0.001, max_rows=2048)
     T = 300
     x = synth.gen_x(77, T, dev)
-    ref = lay.prefill(x).clone()                              # eager (also sets up the library GEMM plans for T)
+    ref = lay.prefill(x).clone()                              # eager
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
