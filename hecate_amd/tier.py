@@ -113,6 +113,100 @@ def load_reference_int4(u4dir, layer, experts, device):
     return bank
 
 
+def reference_canonical(u4dir, layer, experts):
+    """the same files as load_reference_int4, as the host-CPU tier takes them (CpuTier.add_layer): per expert a dict
+    of canonical row-major codes {gate,up,down}_q u8 [N, K/2] (low nibble = even k) and bf16 group scales
+    {m}_s u16 [N, K/128], every group = bf16(row scale) (tier_split.py:246-250 makes its Grace copies row-major)"""
+    bank = load_reference_int4(u4dir, layer, experts, "cpu")
+    out = []
+    for j in range(len(experts)):
+        ex = {}
+        for m, (N, K) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
+            q = bank.view(f"{m}_q", j).numpy()
+            s = bank.view(f"{m}_s", j).numpy()
+            c = np.empty((N, K // 2), np.uint8)
+            sc = np.empty((N, K // 128), np.uint16)
+            call("hmoe_unpack_i4", q.ctypes.data, s.ctypes.data, N, K, c.ctypes.data, sc.ctypes.data)
+            ex[m + "_q"], ex[m + "_s"] = c, sc
+        out.append(ex)
+    return out
+
+
+class Placement:
+    """one layer of the reference's placement file (tier_split.py:18, written by tools/placement/tier_placement.py:
+    15-18): local expert j is original expert perm[j]; [0, hot) int4 on the accelerator, [hot, hot + far) int4 on
+    the host CPU, [first, E) the reference's third band (3-bit trellis on a second GPU, not built here)"""
+
+    def __init__(self, perm, hot, far, first):
+        self.perm, self.hot, self.far, self.first = list(perm), int(hot), int(far), int(first)
+
+    def __repr__(self):
+        return f"Placement(hot={self.hot}, far={self.far}, first={self.first}, E={len(self.perm)})"
+
+
+def load_placement(src):
+    """the placement file {layer: {"perm": [E ids], "hot": n, "far": m, "first": n + m}} (a path, JSON text or the
+    parsed dict) -> {layer (int): Placement}, checked as the reference loads it: "hot" and "far" default to 0
+    (tier_split.py:174 p.get), perm is a permutation of 0 .. E - 1, hot + far <= first <= E, and a layer whose
+    first reaches E (no third band, the MTP layer) keeps the identity order (tier_split.py:177)"""
+    import json
+    import os
+    if isinstance(src, dict):
+        raw = src
+    elif isinstance(src, str) and os.path.exists(src):
+        with open(src) as f:
+            raw = json.load(f)
+    else:
+        raw = json.loads(src)
+    out = {}
+    for key, p in raw.items():
+        try:
+            L = int(key)
+        except (TypeError, ValueError):
+            raise ValueError(f"placement: layer key {key!r} is not an integer") from None
+        if not isinstance(p, dict) or "perm" not in p or "first" not in p:
+            raise ValueError(f"placement: layer {L} needs 'perm' and 'first'")
+        perm = [int(e) for e in p["perm"]]
+        E = len(perm)
+        if sorted(perm) != list(range(E)):
+            raise ValueError(f"placement: layer {L} perm is not a permutation of 0..{E - 1}")
+        hot, far, first = int(p.get("hot", 0)), int(p.get("far", 0)), int(p["first"])
+        if hot < 0 or far < 0 or hot + far > min(first, E):
+            raise ValueError(f"placement: layer {L} hot {hot} far {far} first {first} (E {E})")
+        if first >= E and perm != list(range(E)):
+            raise ValueError(f"placement: layer {L} has no third band but a permuted order (tier_split.py:177)")
+        out[L] = Placement(perm, hot, far, first)
+    return out
+
+
+def layer_from_reference(place, u4dir, wg, bias, device, shared=None, cpu=None, max_rows=16):
+    """one layer as tier_split_load builds it (tier_split.py:171-269) from a Placement and the reference's int4 files
+    (u4dir/layer{L}*.safetensors): router rows and bias permuted to the placement order (rtx_split.py:5,116: local id
+    j = original expert perm[j]; wg fp32 [E, H] and bias [E] in the original order), experts perm[0:hot] resident on
+    the GPU (load_reference_int4), perm[hot:hot + far] added to the host-CPU tier `cpu` (a CpuTier, if given) as
+    layer `place.layer`. Picks of local ids >= hot contribute nothing on the GPU (the partial of the tier split).
+    place: a Placement with a .layer attribute, or (layer, Placement)."""
+    if isinstance(place, tuple):
+        layer, place = place
+    else:
+        layer = place.layer
+    if place.hot < 1 or place.first != place.hot + place.far:
+        raise ValueError(f"layer {layer}: the int4 tiers need hot > 0 and first == hot + far "
+                         f"(tier_split.py:189), got {place}")
+    dev = torch.device(device)
+    if wg.shape[0] != len(place.perm) or bias.numel() != len(place.perm):
+        raise ValueError(f"layer {layer}: router of {wg.shape[0]} experts for a placement of {len(place.perm)}")
+    idx = torch.tensor(place.perm, dtype=torch.int64, device=wg.device)
+    wg_p = wg.index_select(0, idx).contiguous().to(dev)
+    b_p = bias.reshape(-1).index_select(0, idx).contiguous().to(dev)
+    bank = load_reference_int4(u4dir, layer, place.perm[:place.hot], dev)
+    lay = MoELayer(wg_p, b_p, bank, shared, lo=0, n_hot=place.hot, max_rows=max_rows)
+    lay.perm, lay.place, lay.layer = place.perm, place, layer
+    if place.far and cpu is not None:
+        cpu.add_layer(layer, place.hot, reference_canonical(u4dir, layer, place.perm[place.hot:place.first]))
+    return lay
+
+
 def f16t_rows(t, N, K):
     """an F16T matrix (1 KB tiles of 16 rows x 32 k, include/hecate_moe.h) as row-major f16 [N, K]: tile (nb, ks),
     lane l = 16 j + r holds row 16 nb + r at k = 32 ks + 8 j .. + 8"""

@@ -88,6 +88,26 @@ def test_router_bit_exact(dev, R, bias_sigma):
     assert np.array_equal(u16(xh), O.f32_to_f16(O.bf16_to_f32(x)))
 
 
+@pytest.mark.parametrize("R", [4, 20])
+def test_router_forced_tie_lowest_index(dev, R):
+    """the forced tie of the oracle's test at the top-8 boundary through both router paths (R <= 16, R > 16): an
+    exact tie of experts 40 and 41 picks 40, a key one or two ulps higher picks its expert; bit-exact with the
+    oracle"""
+    from test_oracle import forced_tie_router
+    for lo, hi, near in ((40, 41, False), (41, 40, False), (40, 41, True), (41, 40, True)):
+        x, wg, bias = forced_tie_router(R, lo, hi, near)
+        sel_ref, rw_ref = O.router(x, wg, bias)
+        xt = torch.from_numpy(x.view(np.int16)).to(dev).view(torch.bfloat16)
+        logits, ctr = router.buffers(R, dev)
+        sel = torch.empty((R, 8), dtype=torch.int64, device=dev)
+        rw = torch.empty((R, 8), dtype=torch.float16, device=dev)
+        router.router_fused(xt, torch.from_numpy(wg).to(dev), torch.from_numpy(bias).to(dev), logits, ctr, sel, rw,
+                            8, 2.5)
+        torch.cuda.synchronize()
+        assert np.array_equal(sel.cpu().numpy(), sel_ref) and np.array_equal(u16(rw), rw_ref)
+        assert all(r[7] == (hi if near else 40) for r in sel_ref)
+
+
 # ---- decode ------------------------------------------------------------------------------------------------------
 
 _LAYERS = {}
@@ -720,3 +740,50 @@ def test_stack_16_layers_b4(dev):
         torch.cuda.synchronize()
     del st, layers
     torch.cuda.empty_cache()
+
+
+# ---- reference-format ingest: a layer from the placement file and the reference's int4 files ----------------------
+
+def test_layer_from_reference_files(dev, tmp_path):
+    """tier_split_load (tier_split.py:171-269) restated: a placement (hot 4 of a random permutation) and the
+    reference's int4 files (fragment-order codes, fp32 row scales) give a GPU layer whose decode (R = 4) and prefill
+    (T = 64) partials match the oracle's exact mode on the files' codes with the row scale in every group; routing
+    (router rows and bias permuted to the placement order) bit-exact. The bias lifts the four hot experts into every
+    row's top-8."""
+    from test_placement import write_reference_files
+    L, HOT = 6, 4
+    perm = [int(e) for e in np.random.default_rng(17).permutation(E)]
+    place = tier.load_placement({str(L): {"perm": perm, "hot": HOT, "far": 0, "first": HOT}})
+    canon = write_reference_files(tmp_path, L, perm[:HOT], 41)
+    bias = np.zeros(E, np.float32)
+    bias[perm[:HOT]] = 2.0
+    wg, b = synth.router_weights(L, dev, bias=bias)
+    lay = tier.layer_from_reference((L, place[L]), str(tmp_path), wg, b, dev, max_rows=64)
+    hl = HostLayer(L, bias=bias, perm=perm, n_hot=HOT, shared=False)
+    table = O.ExpertTable([canon[perm[j]] for j in range(HOT)])
+    for T in (4, 64):
+        log(f"reference-file layer, {T} rows")
+        x = synth.gen_x(900 + T, T, dev)
+        xn = u16(x)
+        if T <= 16:
+            y = decode_fp32(lay, x, dev, with_shared=False)
+            sel, rw = lay.sel[:T].cpu().numpy(), u16(lay.rw[:T])
+        else:
+            lay.prefill(x, with_shared=False)
+            pf = lay._pf
+            y = pf.y[:T]
+            y.zero_()
+            lay.prefill_experts(pf.xh[:T], y, with_shared=False)
+            torch.cuda.synchronize()
+            sel, rw = pf.sel[:T].cpu().numpy(), u16(pf.rw[:T])
+            y = y.clone()
+            pf.y[:T].zero_()
+        sel_ref, rw_ref = hl.route(xn)
+        assert np.array_equal(sel, sel_ref) and np.array_equal(rw, rw_ref)
+        assert all(np.isin(np.arange(HOT), sel_ref[r]).all() for r in range(T))
+        # (the oracle takes up to 16 rows a call)
+        ref = np.concatenate([O.moe(0, xn[r:r + 16], sel_ref[r:r + 16], rw_ref[r:r + 16], table, 0, HOT, None,
+                                    threads=16) for r in range(0, T, 16)])
+        ma, mr = parity(y.cpu().numpy(), ref)
+        log(f"  max|d| {ma:.3e} mean-rel {mr:.3e}")
+        assert ma <= MAX_ABS and mr <= MEAN_REL

@@ -160,6 +160,34 @@ def test_router_select_bias_zero_is_topk_of_logits_and_ties_lowest_index():
     assert list(sel[0]) == [3, 5, 77, 200, 0, 1, 2, 4]
 
 
+def forced_tie_router(R, lo, hi, near):
+    """a router whose experts lo and hi have identical rows and sit at the top-8 boundary: seven experts (100..106)
+    far ahead by bias, lo and hi next with bias 3 (selection keys in [3, 4), where the fp32 step is 2^-22), everything
+    else behind. near: hi's bias two steps up, so hi's key is one or two ulps above lo's (one step alone can round to
+    the same key when act + 3 falls halfway between two)."""
+    rng = np.random.default_rng(23)
+    wg = (rng.standard_normal((256, 6144)) * 0.0013).astype(np.float32)
+    wg[hi] = wg[lo]
+    bias = np.zeros(256, np.float32)
+    bias[100:107] = 5.0
+    bias[lo] = 3.0
+    bias[hi] = np.float32(3.0 + 2.0 ** -21) if near else 3.0
+    x = O.f32_to_bf16(rng.standard_normal((R, 6144)).astype(np.float32))
+    return x, wg, bias
+
+
+@pytest.mark.parametrize("lo,hi", [(40, 41), (41, 40)])
+def test_router_forced_tie_takes_the_lowest_index(lo, hi):
+    """exl3_router.py:106-121 / nr4_kernel.cuh:307-366: keys descending, then the lowest expert index. An exact tie
+    at the 8th place goes to min(lo, hi); a key one ulp higher wins whatever its index"""
+    x, wg, bias = forced_tie_router(6, lo, hi, near=False)
+    sel, _ = O.router(x, wg, bias)
+    assert all(sorted(r[:7]) == list(range(100, 107)) and r[7] == min(lo, hi) for r in sel)
+    x, wg, bias = forced_tie_router(6, lo, hi, near=True)
+    sel, _ = O.router(x, wg, bias)
+    assert all(r[7] == hi for r in sel)
+
+
 # ---- dispatch -----------------------------------------------------------------------------------------------------
 
 def test_dispatch_is_stable_argsort_bincount():
