@@ -68,7 +68,7 @@ __global__ void gen_i4_kernel(uint64_t key_q, uint64_t key_s, float sigma_s, int
         if (l < 16)
         {
             const int r = nb * 16 + l;
-            s[(size_t) r * KG + kg] = hmoe_f2bf(fabsf(sigma_s * hmoe_normal(key_s, (uint64_t) r * KG + kg)));
+            s[sc_index(r, kg, KG)] = hmoe_f2bf(fabsf(sigma_s * hmoe_normal(key_s, (uint64_t) r * KG + kg)));
         }
     }
 }
@@ -117,7 +117,7 @@ __global__ void dequant_kernel(const u32x4* __restrict__ q, const uint16_t* __re
         const size_t tile = i >> 6;
         const int kg = (int) (tile % KG), nb = (int) (tile / KG);
         const int row = nb * 16 + (l & 15);
-        const float sc = bf2f(s[(size_t) row * KG + kg]);
+        const float sc = bf2f(s[sc_index(row, kg, KG)]);
         const u32x4 v = q[i];
         const DqConsts dq = dq_consts();
         #pragma unroll
@@ -207,7 +207,7 @@ extern "C" int hmoe_version(void) { return 1; }
 extern "C" int hmoe_pack_i4(const uint8_t* codes, const uint16_t* scales, int N, int K, void* q_host, void* s_host)
 {
     HMOE_REQUIRE(codes && scales && q_host && s_host, "pack_i4: null buffer");
-    HMOE_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 128 == 0, "pack_i4: shape %d x %d", N, K);
+    HMOE_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 512 == 0, "pack_i4: shape %d x %d", N, K);
     const int KG = K / 128;
     uint32_t* q = (uint32_t*) q_host;
     uint16_t* s = (uint16_t*) s_host;
@@ -224,14 +224,15 @@ extern "C" int hmoe_pack_i4(const uint8_t* codes, const uint16_t* scales, int N,
                     q[(tile * 64 + l) * 4 + j] = word;
                 }
         }
-    memcpy(s, scales, sizeof(uint16_t) * (size_t) N * KG);       // scales keep the canonical row-major layout
+    for (int n = 0; n < N; ++n)
+        for (int g = 0; g < KG; ++g) s[sc_index(n, g, KG)] = scales[(size_t) n * KG + g];
     return HMOE_OK;
 }
 
 extern "C" int hmoe_unpack_i4(const void* q_host, const void* s_host, int N, int K, uint8_t* codes, uint16_t* scales)
 {
     HMOE_REQUIRE(codes && scales && q_host && s_host, "unpack_i4: null buffer");
-    HMOE_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 128 == 0, "unpack_i4: shape %d x %d", N, K);
+    HMOE_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 512 == 0, "unpack_i4: shape %d x %d", N, K);
     const int KG = K / 128;
     const uint32_t* q = (const uint32_t*) q_host;
     const uint16_t* s = (const uint16_t*) s_host;
@@ -253,7 +254,8 @@ extern "C" int hmoe_unpack_i4(const void* q_host, const void* s_host, int N, int
                     }
                 }
         }
-    memcpy(scales, s, sizeof(uint16_t) * (size_t) N * KG);
+    for (int n = 0; n < N; ++n)
+        for (int g = 0; g < KG; ++g) scales[(size_t) n * KG + g] = s[sc_index(n, g, KG)];
     return HMOE_OK;
 }
 
@@ -279,7 +281,7 @@ extern "C" int hmoe_pack_dense(const uint16_t* w, int N, int K, uint16_t* out)
 extern "C" int hmoe_repack_moe4(const uint8_t* frag, const float* row_scale, int N, int K, void* q_host, void* s_host)
 {
     HMOE_REQUIRE(frag && row_scale && q_host && s_host, "repack_moe4: null buffer");
-    HMOE_REQUIRE(N > 0 && K > 0 && N % 64 == 0 && K % 128 == 0, "repack_moe4: shape %d x %d", N, K);
+    HMOE_REQUIRE(N > 0 && K > 0 && N % 64 == 0 && K % 512 == 0, "repack_moe4: shape %d x %d", N, K);
     const int KB = K / 64, KG = K / 128;
     uint8_t* codes = (uint8_t*) calloc((size_t) N * K / 2, 1);
     uint16_t* sc = (uint16_t*) malloc(sizeof(uint16_t) * (size_t) N * KG);
@@ -317,7 +319,7 @@ extern "C" int hmoe_repack_moe4(const uint8_t* frag, const float* row_scale, int
 extern "C" int hmoe_gen_i4(uint64_t key_q, uint64_t key_s, float sigma_s, int N, int K, void* q, void* s, void* stream)
 {
     HMOE_REQUIRE(q && s, "gen_i4: null buffer");
-    HMOE_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 128 == 0, "gen_i4: shape %d x %d", N, K);
+    HMOE_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 512 == 0, "gen_i4: shape %d x %d", N, K);
     const size_t lanes = (size_t) (N / 16) * (K / 128) * 64;
     gen_i4_kernel<<<grid_for(lanes, 256), 256, 0, (hipStream_t) stream>>>(key_q, key_s, sigma_s, N, K, (u32x4*) q,
                                                                            (uint16_t*) s);
@@ -344,7 +346,7 @@ extern "C" int hmoe_gen_normal(uint64_t key, int64_t n, float mean, float sigma,
 extern "C" int hmoe_moe4_dequant(const void* q, const void* s, int N, int K, uint16_t* out, void* stream)
 {
     HMOE_REQUIRE(q && s && out, "moe4_dequant: null buffer");
-    HMOE_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 128 == 0, "moe4_dequant: shape %d x %d", N, K);
+    HMOE_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 512 == 0, "moe4_dequant: shape %d x %d", N, K);
     const size_t lanes = (size_t) (N / 16) * (K / 128) * 64;
     dequant_kernel<<<grid_for(lanes, 256), 256, 0, (hipStream_t) stream>>>((const u32x4*) q, (const uint16_t*) s, N, K,
                                                                            (_Float16*) out);

@@ -258,7 +258,7 @@ __global__ void __launch_bounds__(GW * 64) gu7_kernel(
     auto load = [&](GuItem& S, int i) {
         const int it = b + min(i, max(nr - 1, 0)) * G, j = min(it / NB_I, max(m - 1, 0)), nb = it - (it / NB_I) * NB_I;
         const size_t toff = ((size_t) (nb * KG_H + 4 * w) * 64 + l) * 16;
-        const size_t soff = ((size_t) (nb * 16 + row) * KG_H + 4 * w) * 2;
+        const size_t soff = sc_index(nb * 16 + row, 4 * w, KG_H) * 2;
         const int kst = i < nr ? 1024 : 0;
         #pragma unroll
         for (int k = 0; k < 4; ++k)
@@ -465,7 +465,7 @@ __global__ void __launch_bounds__(DW * 64) dn6_kernel(
         const int jj = max(min(j, m - 1), 0), nbb = ok ? nb : 0;
         // (offsets in 32-bit arithmetic, zero-extended per item: a 64-bit lane term would stay live across the loop)
         const size_t toff = (uint32_t) (((nbb * KG_I + 4 * kq) * 64 + l) * 16);
-        const size_t soff = (uint32_t) (((nbb * 16 + (l & 15)) * KG_I + 4 * kq) * 2);
+        const size_t soff = (uint32_t) (sc_index(nbb * 16 + (l & 15), 4 * kq, KG_I) * 2);
         const int kst = (ok && i < nr) ? 1024 : 0;
         #pragma unroll
         for (int k = 0; k < 4; ++k) S.d[k] = ldw16(ptr[0][jj] + toff + k * kst);

@@ -23,6 +23,13 @@ constexpr int REC_SLOT = SHP_SLOT + 4;      // the gate/up launch's routing reco
 constexpr int ACT_SLOTS = REC_SLOT + 1;
 constexpr int REC_E = 64;                   // record: word 0 = distinct experts m, words REC_E + j = local id of slot j
 
+// I4G128 group scales: 128-byte blocks of 16 rows x 4 k groups; the index (in bf16 units) of row n's scale of group g
+// (KG = K / 128 groups, a multiple of 4)
+__host__ __device__ __forceinline__ size_t sc_index(int n, int g, int KG)
+{
+    return ((size_t) (n >> 4) * (KG >> 2) + (g >> 2)) * 64 + (n & 15) * 4 + (g & 3);
+}
+
 // ---- error state of the C ABI (common.hip) ----
 int set_error(int code, const char* fmt, ...);
 // the prefill shared expert (shared_gemm.hip), f16 row-major operands: act [T][I] = f16(silu(wg x) (wu x)), and

@@ -232,7 +232,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                 {
                     const int nb = nb0 + st;
                     ring[s].q[st][m] = ldw16(wp[m] + ((size_t) (nb * KG + kg) * 64 + l) * 16);
-                    ring[s].s[st][m] = ldg<uint16_t>(sp[m] + ((size_t) (nb * 16 + row) * KG + kg) * 2);
+                    ring[s].s[st][m] = ldg<uint16_t>(sp[m] + sc_index(nb * 16 + row, kg, KG) * 2);
                 }
         };
         f32x4 acc[NS][NMAT][NTT];

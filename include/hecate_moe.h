@@ -12,11 +12,12 @@
  *   - every entry point returns HMOE_OK or an error code; hmoe_last_error() gives the thread's last message.
  *
  * Formats (this build's gfx950 layouts, hmoe_pack_* produce them from the canonical row-major ones):
- *   I4G128 int4 matrix [N][K] (N % 16 == 0, K % 128 == 0): codes in 1 KB tiles of 16 rows x 128 k, tile (nb, kg) at
+ *   I4G128 int4 matrix [N][K] (N % 16 == 0, K % 512 == 0): codes in 1 KB tiles of 16 rows x 128 k, tile (nb, kg) at
  *          byte (nb * K/128 + kg) * 1024; lane l (0..63) of a tile holds 16 bytes = 4 dwords, dword j packs the 8 codes
  *          (q + 8) of row nb*16 + l%16 at k = kg*128 + 32j + 8(l/16) + e, e = 0..7, code e at bit 4(e/2) + 16(e%2).
- *          Scales bf16 [N][K/128], row-major (the canonical layout: a lane that owns row n reads the group scales of
- *          several k groups with one load).
+ *          Scales bf16, N x K/128 of them in 128-byte blocks of 16 rows x 4 k groups: the scale of row n, group g at
+ *          byte ((n/16) * K/512 + g/4) * 128 + (n%16) * 8 + (g%4) * 2, so the 16 rows of a tile read their scales of
+ *          one to four groups from one 128-byte line.
  *   F16T   dense matrix [N][K] (K % 32 == 0) as f16 in 1 KB tiles of 16 rows x 32 k, tile (nb, ks) at byte
  *          (nb * K/32 + ks) * 1024, lane l holds the 8 f16 of row nb*16 + l%16 at k = ks*32 + 8(l/16) + e.
  *   x      bf16 [R][H] (the MoE input); xh its f16 copy (exact for the reference's fp16 activation range).
@@ -54,7 +55,7 @@ int hmoe_version(void);
 
 /* ---- formats (host) ------------------------------------------------------------------------------------------ */
 /* canonical int4 (codes uint8 [N][K/2], code = q + 8, low nibble = even k, as runtime/tier/cpuband.cpp:3-4 and
- * tier_split.py:104-106; scales bf16 [N][K/128]) -> I4G128. Replaces the reference's pack_u4
+ * tier_split.py:104-106; scales bf16 [N][K/128] row-major) -> I4G128. Replaces the reference's pack_u4
  * (tools/quant/gptq_int4.py:74-77) for this build's layout. */
 int hmoe_pack_i4(const uint8_t* codes_host, const uint16_t* scales_host, int N, int K, void* q_host, void* s_host);
 /* inverse of hmoe_pack_i4 (tier_split.py:98-101 _unpack_moe4 is the reference's inverse of its own packing) */

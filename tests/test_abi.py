@@ -59,7 +59,7 @@ def test_empty_prefill_chunk_is_a_no_op():
     assert L.hmoe_moe4p_forward(*args) != 0 and b"null" in L.hmoe_last_error()
 
 
-@pytest.mark.parametrize("N,K", [(16, 128), (64, 384), (2048, 6144)])
+@pytest.mark.parametrize("N,K", [(16, 512), (64, 1536), (2048, 6144)])
 def test_pack_unpack_round_trip_and_layout(N, K):
     rng = np.random.default_rng(N)
     codes = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
@@ -70,13 +70,17 @@ def test_pack_unpack_round_trip_and_layout(N, K):
     _lib.call("hmoe_unpack_i4", q.ctypes.data, s.ctypes.data, N, K, c2.ctypes.data, s2.ctypes.data)
     assert np.array_equal(c2, codes) and np.array_equal(s2, scales)
     # layout: lane l of tile (nb, kg), dword j, element e holds (row nb*16 + l%16, k = kg*128 + 32j + 8(l/16) + e)
-    # at bit 4(e/2) + 16(e%2); scales row-major [N][K/128]
+    # at bit 4(e/2) + 16(e%2); scales in 128-byte blocks of 16 rows x 4 groups (row-major inside a block)
     w = q.view(np.uint32).reshape(N // 16, K // 128, 64, 4)
     full = np.stack([codes & 15, codes >> 4], -1).reshape(N, K)
     for nb, kg, l, j, e in [(0, 0, 0, 0, 0), (0, 0, 17, 2, 5), (N // 16 - 1, K // 128 - 1, 63, 3, 7), (0, 0, 35, 1, 1)]:
         row, k = nb * 16 + l % 16, kg * 128 + 32 * j + 8 * (l // 16) + e
         assert (w[nb, kg, l, j] >> (4 * (e // 2) + 16 * (e % 2))) & 15 == full[row, k]
-    assert np.array_equal(s.reshape(N, K // 128), scales)
+    KG = K // 128
+    blocks = s.reshape(N // 16, KG // 4, 16, 4)
+    assert np.array_equal(blocks.transpose(0, 2, 1, 3).reshape(N, KG), scales)
+    for n, g in [(0, 0), (5, 3), (N - 1, KG - 1), (min(17, N - 1), KG // 2)]:
+        assert s[((n // 16) * (KG // 4) + g // 4) * 64 + (n % 16) * 4 + g % 4] == scales[n, g]
 
 
 def test_pack_dense_is_f16_tiles():
@@ -111,7 +115,7 @@ def test_repack_reference_moe4_weights():
     """tools/quant/gptq_int4.py:74-77 pack_u4 (the reference's fragment order, restated as a permutation of the
     code tensor) + fp32 row scales -> this build's I4G128: same codes, scale = bf16(row scale) in every group"""
     rng = np.random.default_rng(3)
-    N, K = 128, 256
+    N, K = 128, 512
     codes = rng.integers(0, 16, (N, K), dtype=np.uint8)
     frag = _pack_u4_reference_order(codes)
     rs = (rng.random(N) * 0.01).astype(np.float32)
