@@ -95,19 +95,31 @@ __global__ void __launch_bounds__(DBLK) disp_place_kernel(const int64_t* __restr
 // ---------------------------------------------------------------------------------------------------------------
 struct Block { int e, p0, rows; };
 
-// row block blockIdx.x of the plan: up to 2 PB picks (the dispatch's bm <= 256), run as halves of <= PB picks
-__device__ __forceinline__ bool get_block(const int* rbt, int nrb, const int* meta, int n_tab, Block& b)
+// The workgroup's row block and column block. The dispatcher deals a launch's workgroups round-robin over the 8
+// XCDs (workgroup i runs on XCD i % 8), each with its own L2: the column blocks of one row block go to consecutive
+// workgroups of one XCD, so they run together and read the block's input rows from that XCD's L2 (one fetch from
+// memory instead of one per column block). The grid's x extent is a multiple of 8 (pgemm_grid).
+__device__ __forceinline__ void xcd_tile(int& rb, int& cb)
 {
-    const int rb = blockIdx.x;
+    const int i = blockIdx.x + gridDim.x * blockIdx.y, j = i >> 3, ny = gridDim.y;
+    rb = (j / ny) * 8 + (i & 7);
+    cb = j % ny;
+}
+
+static dim3 pgemm_grid(int nrb, int ny) { return dim3((nrb + 7) & ~7, ny); }
+
+// row block rb of the plan: up to 2 PB picks (the dispatch's bm <= 256), run as halves of <= PB picks
+__device__ __forceinline__ bool get_block(const int* rbt, int nrb, const int* meta, int n_tab, int rb, Block& b)
+{
     if (rb >= nrb || (meta && rb >= meta[1])) return false;
     b.e = rbt[4 * rb]; b.p0 = rbt[4 * rb + 1]; b.rows = min(rbt[4 * rb + 2], 2 * PB);
     return b.e >= 0 && b.e < n_tab && b.rows > 0;
 }
 
 // A pipelined grouped GEMM for both projections. Workgroup = (row block of <= 128 picks of one expert, 64 NS output
-// columns); wave w owns output strips nb0 = 4 NS blockIdx.y + NS w .. + NS (16 rows each) of NMAT matrices (gate and
-// up: NS = 2, or down: NS = 4), so every wave holds 4 weight fragments per k step and reads each 16-pick input
-// fragment from LDS once for 4 MFMAs. Per 128-k group kg:
+// columns); wave w of column block cb owns output strips nb0 = NWV NS cb + NS w .. + NS (16 rows each) of NMAT
+// matrices (gate and up: NS = 2, or down: NS = 4), so every wave holds 4 weight fragments per k step and reads each
+// 16-pick input fragment from LDS once for 4 MFMAs. Per 128-k group kg:
 //   * the block's input rows are staged in LDS as f16 by direct global-to-LDS loads (double-buffered, one barrier
 //     per group): the next group's rows load while this group computes;
 //   * the weight tiles come from a ring of D groups of unconditional 16-byte loads (and the lane's row scale), issued
@@ -147,8 +159,10 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
     // while one computes
     __shared__ __attribute__((aligned(16))) u32x4 xs0[NTT * 4 * 64];
     __shared__ __attribute__((aligned(16))) u32x4 xs1[NTT * 4 * 64];
+    int rbi, cbi;
+    xcd_tile(rbi, cbi);
     Block rb;
-    if (!get_block(rbt, nrb, meta, n_tab, rb)) return;
+    if (!get_block(rbt, nrb, meta, n_tab, rbi, rb)) return;
     // a block of more than PBX picks runs as passes of PBX, one after the other (a later pass reads the weights
     // again, mostly from the caches); the barrier between them keeps one pass's last LDS reads ahead of the next
     // pass's first staging
@@ -158,7 +172,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
         const Block b = {rb.e, rb.p0 + h0, min(PBX, rb.rows - h0)};
         const int t = threadIdx.x, l = t & 63, row = l & 15;
         const int w = __builtin_amdgcn_readfirstlane(t >> 6);   // wave index, kept in a scalar register
-        const int nb0 = (blockIdx.y * NWV + w) * NS;
+        const int nb0 = (cbi * NWV + w) * NS;
         const uint8_t* wp[NMAT];
         const uint8_t* sp[NMAT];
         #pragma unroll
@@ -472,13 +486,13 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
     // (inv given) or added into out[tok] by its epilogue (no inverse map: the atomic combine of p4_fin_kernel)
     if (nrb > 0)
     {
-        pgemm_kernel<2, 2, 3><<<dim3(nrb, I / 128), PT, 0, st>>>((const _Float16*) xb, tok, wt, rbt, nrb, meta,
+        pgemm_kernel<2, 2, 3><<<pgemm_grid(nrb, I / 128), PT, 0, st>>>((const _Float16*) xb, tok, wt, rbt, nrb, meta,
             n_tab, gw, uw, gs, us, a, nullptr, T, 0);
         if (inv)
-            pgemm_kernel<1, 4, 2><<<dim3(nrb, H / 256), PT, 0, st>>>(a, nullptr, nullptr, rbt, nrb, meta, n_tab, dw,
+            pgemm_kernel<1, 4, 2><<<pgemm_grid(nrb, H / 256), PT, 0, st>>>(a, nullptr, nullptr, rbt, nrb, meta, n_tab, dw,
                 nullptr, ds, nullptr, nullptr, d, T, 0);
         else
-            pgemm_kernel<1, 4, 2, EPI_FIN><<<dim3(nrb, H / 256), PT, 0, st>>>(a, tok, nullptr, rbt, nrb, meta, n_tab,
+            pgemm_kernel<1, 4, 2, EPI_FIN><<<pgemm_grid(nrb, H / 256), PT, 0, st>>>(a, tok, nullptr, rbt, nrb, meta, n_tab,
                 dw, nullptr, ds, nullptr, nullptr, nullptr, T, 0, out);
     }
     const bool sh = sh_gw != nullptr;
@@ -578,14 +592,14 @@ extern "C" int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid,
     {
         // 256-pick blocks in one pass: 8 waves, each one 16-row strip of gate and of up (or two of down) against the
         // block's 16 pick tiles
-        pgemm_kernel<2, 1, 4, EPI_ACT, 16, 8><<<dim3(nrb, I / 128), 512, 0, st>>>(xh, tok, wt, rbt, nrb, meta, n_tab,
+        pgemm_kernel<2, 1, 4, EPI_ACT, 16, 8><<<pgemm_grid(nrb, I / 128), 512, 0, st>>>(xh, tok, wt, rbt, nrb, meta, n_tab,
             gw, uw, gs, us, (_Float16*) ar, nullptr, T, 0);
         // (d held the f16 copy of x, which the gate/up GEMM has consumed by now: the down rows may overwrite it)
         if (inv)
-            pgemm_kernel<1, 2, 4, EPI_D, 16, 8><<<dim3(nrb, H / 256), 512, 0, st>>>((const _Float16*) ar, nullptr,
+            pgemm_kernel<1, 2, 4, EPI_D, 16, 8><<<pgemm_grid(nrb, H / 256), 512, 0, st>>>((const _Float16*) ar, nullptr,
                 nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, d, T, 0);
         else
-            pgemm_kernel<1, 2, 4, EPI_FIN, 16, 8><<<dim3(nrb, H / 256), 512, 0, st>>>((const _Float16*) ar, tok,
+            pgemm_kernel<1, 2, 4, EPI_FIN, 16, 8><<<pgemm_grid(nrb, H / 256), 512, 0, st>>>((const _Float16*) ar, tok,
                 nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, nullptr, T, 0, out);
     }
     if (inv) pfin_kernel<<<T, 256, 0, st>>>(d, inv, topk, -1, out);
@@ -603,10 +617,10 @@ extern "C" int hmoe_moe4t_gemm(const void* xs, int rows, const int* rbt, int nrb
     if (nrb == 0) return HMOE_OK;
     hipStream_t st = (hipStream_t) stream;
     if (down)
-        pgemm_kernel<1, 4, 2><<<dim3(nrb, H / 256), PT, 0, st>>>((const _Float16*) xs, nullptr, nullptr, rbt, nrb,
+        pgemm_kernel<1, 4, 2><<<pgemm_grid(nrb, H / 256), PT, 0, st>>>((const _Float16*) xs, nullptr, nullptr, rbt, nrb,
             nullptr, n_tab, w0, nullptr, s0, nullptr, nullptr, out, rows, 0);
     else
-        pgemm_kernel<2, 2, 3, EPI_RAW><<<dim3(nrb, I / 128), PT, 0, st>>>((const _Float16*) xs, nullptr, nullptr,
+        pgemm_kernel<2, 2, 3, EPI_RAW><<<pgemm_grid(nrb, I / 128), PT, 0, st>>>((const _Float16*) xs, nullptr, nullptr,
             rbt, nrb, nullptr, n_tab, w0, w1, s0, s1, nullptr, out, rows, 0, nullptr, ps);
     return HMOE_LAUNCHED("moe4t_gemm");
 }
