@@ -292,19 +292,48 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                         #pragma unroll
                         for (int m = 0; m < NMAT; ++m)
                             a[st][m] = dq8s(ring[s].q[st][m][k], sh[st][m], dq);
-                    // the k step's input tiles read together (tiles past the block read stale LDS data, never used), so
-                    // the LDS latency is paid once per k step rather than once per tile
-                    f16x8 bvs[NTT];
-                    #pragma unroll
-                    for (int tt = 0; tt < NTT; ++tt) bvs[tt] = as_f16x8(cur[tt * 256 + fo[k]]);
-                    #pragma unroll
-                    for (int tt = 0; tt < NTT; ++tt)
+                    if constexpr (NS * NMAT >= 4)
                     {
-                        if (tt >= ntt) break;
+                        // four MFMAs per pick tile: the tiles are read in one batch (tiles past the block read stale
+                        // LDS data, never used); the compiler places each read next to its tile's MFMAs, and the other
+                        // wave on the SIMD covers that read's latency
+                        f16x8 bvs[NTT];
                         #pragma unroll
-                        for (int st = 0; st < NS; ++st)
+                        for (int tt = 0; tt < NTT; ++tt) bvs[tt] = as_f16x8(cur[tt * 256 + fo[k]]);
+                        #pragma unroll
+                        for (int tt = 0; tt < NTT; ++tt)
+                        {
+                            if (tt >= ntt) break;
                             #pragma unroll
-                            for (int m = 0; m < NMAT; ++m) acc[st][m][tt] = mfma16(a[st][m], bvs[tt], acc[st][m][tt]);
+                            for (int st = 0; st < NS; ++st)
+                                #pragma unroll
+                                for (int m = 0; m < NMAT; ++m)
+                                    acc[st][m][tt] = mfma16(a[st][m], bvs[tt], acc[st][m][tt]);
+                        }
+                    }
+                    else
+                    {
+                        // two MFMAs per pick tile, too few to cover a read's latency: the tiles are read two ahead of
+                        // their MFMAs, and each read is consumed by an empty asm after the MFMAs of the tile before
+                        // it, which keeps the read ahead of the branch that ends the block's tiles (the compiler
+                        // would otherwise sink it behind that branch, next to its MFMAs, and wait out its latency)
+                        f16x8 bq[3];
+                        bq[0] = as_f16x8(cur[fo[k]]);
+                        bq[1] = as_f16x8(cur[256 + fo[k]]);
+                        #pragma unroll
+                        for (int tt = 0; tt < NTT; ++tt)
+                        {
+                            if (tt >= ntt) break;
+                            if (tt + 2 < NTT) bq[2] = as_f16x8(cur[(tt + 2) * 256 + fo[k]]);
+                            #pragma unroll
+                            for (int st = 0; st < NS; ++st)
+                                #pragma unroll
+                                for (int m = 0; m < NMAT; ++m)
+                                    acc[st][m][tt] = mfma16(a[st][m], bq[0], acc[st][m][tt]);
+                            if (tt + 1 < NTT) asm volatile("" :: "v"(bq[1]));
+                            bq[0] = bq[1];
+                            bq[1] = bq[2];
+                        }
                     }
                 }
                 fetch(min(kg + D, KG - 1), sc);                 // refill the slot just used (clamped at the end)
