@@ -292,48 +292,30 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                         #pragma unroll
                         for (int m = 0; m < NMAT; ++m)
                             a[st][m] = dq8s(ring[s].q[st][m][k], sh[st][m], dq);
-                    if constexpr (NS * NMAT >= 4)
+                    // The pick tiles are read PD tiles ahead of their MFMAs (a tile past the block reads stale LDS
+                    // data, never used). Each read is consumed by an empty asm after the MFMAs of the tile before it,
+                    // which keeps the read ahead of the branch that ends the block's tiles: the compiler would
+                    // otherwise sink it behind that branch, next to its MFMAs, and wait out its latency there. With
+                    // four MFMAs per tile one tile ahead is enough and the consuming asm is pinned behind all four
+                    // (measured: -1 %); with two, two tiles ahead and the asm left to the scheduler (-8 % at 8192
+                    // tokens, pinning it cost 1.5 %).
+                    constexpr int PD = NS * NMAT >= 4 ? 1 : 2;
+                    f16x8 bq[PD + 1];
+                    #pragma unroll
+                    for (int i = 0; i < PD; ++i) bq[i] = as_f16x8(cur[i * 256 + fo[k]]);
+                    #pragma unroll
+                    for (int tt = 0; tt < NTT; ++tt)
                     {
-                        // four MFMAs per pick tile: the tiles are read in one batch (tiles past the block read stale
-                        // LDS data, never used); the compiler places each read next to its tile's MFMAs, and the other
-                        // wave on the SIMD covers that read's latency
-                        f16x8 bvs[NTT];
+                        if (tt >= ntt) break;
+                        if (tt + PD < NTT) bq[PD] = as_f16x8(cur[(tt + PD) * 256 + fo[k]]);
                         #pragma unroll
-                        for (int tt = 0; tt < NTT; ++tt) bvs[tt] = as_f16x8(cur[tt * 256 + fo[k]]);
-                        #pragma unroll
-                        for (int tt = 0; tt < NTT; ++tt)
-                        {
-                            if (tt >= ntt) break;
+                        for (int st = 0; st < NS; ++st)
                             #pragma unroll
-                            for (int st = 0; st < NS; ++st)
-                                #pragma unroll
-                                for (int m = 0; m < NMAT; ++m)
-                                    acc[st][m][tt] = mfma16(a[st][m], bvs[tt], acc[st][m][tt]);
-                        }
-                    }
-                    else
-                    {
-                        // two MFMAs per pick tile, too few to cover a read's latency: the tiles are read two ahead of
-                        // their MFMAs, and each read is consumed by an empty asm after the MFMAs of the tile before
-                        // it, which keeps the read ahead of the branch that ends the block's tiles (the compiler
-                        // would otherwise sink it behind that branch, next to its MFMAs, and wait out its latency)
-                        f16x8 bq[3];
-                        bq[0] = as_f16x8(cur[fo[k]]);
-                        bq[1] = as_f16x8(cur[256 + fo[k]]);
+                            for (int m = 0; m < NMAT; ++m) acc[st][m][tt] = mfma16(a[st][m], bq[0], acc[st][m][tt]);
+                        if constexpr (PD == 1) __builtin_amdgcn_sched_barrier(0);
+                        if (tt + 1 < NTT) asm volatile("" :: "v"(bq[1]));
                         #pragma unroll
-                        for (int tt = 0; tt < NTT; ++tt)
-                        {
-                            if (tt >= ntt) break;
-                            if (tt + 2 < NTT) bq[2] = as_f16x8(cur[(tt + 2) * 256 + fo[k]]);
-                            #pragma unroll
-                            for (int st = 0; st < NS; ++st)
-                                #pragma unroll
-                                for (int m = 0; m < NMAT; ++m)
-                                    acc[st][m][tt] = mfma16(a[st][m], bq[0], acc[st][m][tt]);
-                            if (tt + 1 < NTT) asm volatile("" :: "v"(bq[1]));
-                            bq[0] = bq[1];
-                            bq[1] = bq[2];
-                        }
+                        for (int i = 0; i < PD; ++i) bq[i] = bq[i + 1];
                     }
                 }
                 fetch(min(kg + D, KG - 1), sc);                 // refill the slot just used (clamped at the end)
@@ -515,7 +497,7 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
     // (inv given) or added into out[tok] by its epilogue (no inverse map: the atomic combine of p4_fin_kernel)
     if (nrb > 0)
     {
-        pgemm_kernel<2, 2, 3><<<pgemm_grid(nrb, I / 128), PT, 0, st>>>((const _Float16*) xb, tok, wt, rbt, nrb, meta,
+        pgemm_kernel<2, 2, 2><<<pgemm_grid(nrb, I / 128), PT, 0, st>>>((const _Float16*) xb, tok, wt, rbt, nrb, meta,
             n_tab, gw, uw, gs, us, a, nullptr, T, 0);
         if (inv)
             pgemm_kernel<1, 4, 2><<<pgemm_grid(nrb, H / 256), PT, 0, st>>>(a, nullptr, nullptr, rbt, nrb, meta, n_tab, dw,
@@ -649,7 +631,7 @@ extern "C" int hmoe_moe4t_gemm(const void* xs, int rows, const int* rbt, int nrb
         pgemm_kernel<1, 4, 2><<<pgemm_grid(nrb, H / 256), PT, 0, st>>>((const _Float16*) xs, nullptr, nullptr, rbt, nrb,
             nullptr, n_tab, w0, nullptr, s0, nullptr, nullptr, out, rows, 0);
     else
-        pgemm_kernel<2, 2, 3, EPI_RAW><<<pgemm_grid(nrb, I / 128), PT, 0, st>>>((const _Float16*) xs, nullptr, nullptr,
+        pgemm_kernel<2, 2, 2, EPI_RAW><<<pgemm_grid(nrb, I / 128), PT, 0, st>>>((const _Float16*) xs, nullptr, nullptr,
             rbt, nrb, nullptr, n_tab, w0, w1, s0, s1, nullptr, out, rows, 0, nullptr, ps);
     return HMOE_LAUNCHED("moe4t_gemm");
 }
