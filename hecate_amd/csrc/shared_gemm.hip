@@ -19,37 +19,39 @@ namespace hmoe {
 
 enum { DG_ACT = 0, DG_D = 1, DG_ADD = 2 };
 
-template <int NMAT, int TM, int TN, int EPI>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) dgemm_kernel(
+template <int NMAT, int TM, int TN, int WM, int WN, int EPI>
+__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
+dgemm_kernel(
     const _Float16* __restrict__ w0, const _Float16* __restrict__ w1, const _Float16* __restrict__ x, int N, int K,
     void* __restrict__ out, int ldo)
 {
     static_assert((NMAT == 2) == (EPI == DG_ACT), "the SwiGLU epilogue pairs gate and up");
     constexpr int NST = 3;                              // LDS stages, issued NST - 1 ahead
     constexpr int TMO = TM / NMAT;                      // tiles per matrix per wave
-    constexpr int AT = 2 * TM, BT = 2 * TN;             // weight and token tiles of the workgroup
+    constexpr int NW = WM * WN;                         // waves: WM along the weight rows, WN along the tokens
+    constexpr int AT = WM * TM, BT = WN * TN;           // weight and token tiles of the workgroup
     constexpr int NB = (AT + BT) * 2;                   // 1 KB blocks (8 rows x 64 k) per stage
-    constexpr int SL = NB / 4;                          // blocks staged per wave per stage
-    static_assert(NB % 4 == 0 && TM % NMAT == 0 && TM * TN <= 64, "4 waves share the staging; 256 accumulators");
+    constexpr int SL = NB / NW;                         // blocks staged per wave per stage
+    static_assert(NB % NW == 0 && TM % NMAT == 0 && TM * TN <= 64, "the waves share the staging; 256 accumulators");
     __shared__ __attribute__((aligned(16))) u32x4 lds[NST][NB * 64];
     const int t = threadIdx.x, l = t & 63, row = l & 15;
-    const int w = __builtin_amdgcn_readfirstlane(t >> 6), wm = w & 1, wn = w >> 1;
-    const int m0 = blockIdx.x * 2 * 16 * TMO;           // first output row of each matrix
-    const int n0 = blockIdx.y * 2 * 16 * TN;            // first token
+    const int w = __builtin_amdgcn_readfirstlane(t >> 6), wm = w % WM, wn = w / WM;
+    const int m0 = blockIdx.x * WM * 16 * TMO;          // first output row of each matrix
+    const int n0 = blockIdx.y * WN * 16 * TN;           // first token
     const int KS = K / 64;
-    // the blocks this wave stages (b = w + 4 i): block b holds rows 8 b .. + 8 of the stage's tiles (weight tiles
-    // first: tile a = matrix a / (2 TMO), rows 16 (a % (2 TMO)) .., then token tiles); a scalar base per block and the
-    // lane's byte offset from it
+    // the blocks this wave stages (b = w + NW i): block b holds rows 8 b .. + 8 of the stage's tiles (weight tiles
+    // first: tile a = matrix a / (WM TMO), rows 16 (a % (WM TMO)) .., then token tiles); a scalar base per block and
+    // the lane's byte offset from it
     const _Float16* sb[SL];
     uint32_t vo[SL];
     const uint32_t chunk = 16u * (uint32_t) ((l & 7) ^ (l >> 3));
     #pragma unroll
     for (int i = 0; i < SL; ++i)
     {
-        const int b = w + 4 * i, tile = b >> 1, r = 8 * (b & 1) + (l >> 3);
+        const int b = w + NW * i, tile = b >> 1, r = 8 * (b & 1) + (l >> 3);
         if (tile < AT)
         {
-            const int mat = tile / (2 * TMO), tr = tile % (2 * TMO);
+            const int mat = tile / (WM * TMO), tr = tile % (WM * TMO);
             sb[i] = (mat == 0 ? w0 : w1) + (size_t) (m0 + 16 * tr) * K;
             vo[i] = (uint32_t) r * (K * 2) + chunk;
         }
@@ -71,7 +73,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
             const _Float16* base = sb[i] + (live ? 64 * s : 0);
             const uint32_t v = live ? vo[i] : 0u;
             const uint32_t la = __builtin_amdgcn_readfirstlane(
-                (uint32_t) (uintptr_t) (__attribute__((address_space(3))) void*) (buf + (w + 4 * i) * 64));
+                (uint32_t) (uintptr_t) (__attribute__((address_space(3))) void*) (buf + (w + NW * i) * 64));
     #pragma clang diagnostic push
     #pragma clang diagnostic ignored "-Winline-asm"
             asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" :: "v"(v), "s"(base), "s"(la)
@@ -106,7 +108,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
             #pragma unroll
             for (int i = 0; i < TM; ++i)
             {
-                const int tile = (i / TMO) * 2 * TMO + wm * TMO + i % TMO;
+                const int tile = (i / TMO) * WM * TMO + wm * TMO + i % TMO;
                 a[ks][i] = as_f16x8(cur[tile * 128 + fo[ks]]);
             }
             #pragma unroll
@@ -153,8 +155,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
 
 // gate and up: workgroups of 128 act columns x 128 tokens (TM 8 = 4 gate + 4 up tiles, TN 4: I / 128 x T / 128, 256
 // workgroups at 2048 tokens, one per CU); down: 192 output rows x 128 tokens (TM 6, TN 4: 512 workgroups at 2048)
-constexpr int GU_TM = 8, GU_TN = 4;
-constexpr int DN_TM = 6, DN_TN = 4;
+constexpr int GU_TM = 4, GU_TN = 4, GU_WM = 4, GU_WN = 2;
+constexpr int DN_TM = 3, DN_TN = 4, DN_WM = 4, DN_WN = 2;
 
 }  // namespace hmoe
 
@@ -162,22 +164,24 @@ using namespace hmoe;
 
 int hmoe::dense_gate_up(const _Float16* wg, const _Float16* wu, const _Float16* x, int T, _Float16* act, hipStream_t st)
 {
-    constexpr int BM = 32 * GU_TM / 2, BN = 32 * GU_TN;
+    constexpr int BM = 16 * GU_WM * GU_TM / 2, BN = 16 * GU_WN * GU_TN;
     static_assert(I % BM == 0 && H % 64 == 0, "gate/up tiling");
     HMOE_REQUIRE(T >= 1 && ((uintptr_t) wg & 15) == 0 && ((uintptr_t) wu & 15) == 0 && ((uintptr_t) x & 15) == 0 &&
                  ((uintptr_t) act & 7) == 0, "shared gate/up: T %d or alignment", T);
-    dgemm_kernel<2, GU_TM, GU_TN, DG_ACT><<<dim3(I / BM, (T + BN - 1) / BN), 256, 0, st>>>(wg, wu, x, T, H, act, I);
+    dgemm_kernel<2, GU_TM, GU_TN, GU_WM, GU_WN, DG_ACT><<<dim3(I / BM, (T + BN - 1) / BN), 64 * GU_WM * GU_WN, 0, st>>>(
+        wg, wu, x, T, H, act, I);
     return HMOE_LAUNCHED("shared gate/up");
 }
 
 int hmoe::dense_down(const _Float16* wd, const _Float16* act, int T, float* out, bool add, hipStream_t st)
 {
-    constexpr int BM = 32 * DN_TM, BN = 32 * DN_TN;
+    constexpr int BM = 16 * DN_WM * DN_TM, BN = 16 * DN_WN * DN_TN;
     static_assert(H % BM == 0 && I % 64 == 0, "down tiling");
     HMOE_REQUIRE(T >= 1 && ((uintptr_t) wd & 15) == 0 && ((uintptr_t) act & 15) == 0 && ((uintptr_t) out & 15) == 0,
                  "shared down: T %d or alignment", T);
     const dim3 g(H / BM, (T + BN - 1) / BN);
-    if (add) dgemm_kernel<1, DN_TM, DN_TN, DG_ADD><<<g, 256, 0, st>>>(wd, nullptr, act, T, I, out, H);
-    else dgemm_kernel<1, DN_TM, DN_TN, DG_D><<<g, 256, 0, st>>>(wd, nullptr, act, T, I, out, H);
+    constexpr int NT = 64 * DN_WM * DN_WN;
+    if (add) dgemm_kernel<1, DN_TM, DN_TN, DN_WM, DN_WN, DG_ADD><<<g, NT, 0, st>>>(wd, nullptr, act, T, I, out, H);
+    else dgemm_kernel<1, DN_TM, DN_TN, DN_WM, DN_WN, DG_D><<<g, NT, 0, st>>>(wd, nullptr, act, T, I, out, H);
     return HMOE_LAUNCHED("shared down");
 }
