@@ -5,7 +5,7 @@
 //   small (R <= 16): a logits kernel (two experts per workgroup, one 32-element chunk per thread, chunk sums folded
 //                    through LDS) and a select kernel (one wave per row); the kernel boundary replaces the reference's
 //                    last-block counter (exl3_router.py:74-83,130), whose cross-workgroup fences are costly on gfx950.
-//   large (R > 16) : a register-tiled fp32 GEMM per (64 rows, 64 experts, segment) with the same chain order, then a
+//   large (R > 16) : a register-tiled fp32 GEMM per (128 rows, 128 experts, segment) with the same chain order, then a
 //                    select kernel that folds the 8 segment sums and picks each row's top-k (one wave per row).
 #include "hmoe_dev.h"
 
@@ -50,75 +50,105 @@ __global__ void __launch_bounds__(1024) router_select_small_kernel(const float* 
     select_row(logits + (size_t) r * RMAXE, bias, E, topk, scale, sel + (size_t) r * topk, rw + (size_t) r * topk);
 }
 
-// large path, 1: segment sums seg[s][r][e] for a 64-row x 64-expert tile, 4 x 4 outputs per thread
-__global__ void __launch_bounds__(256) router_seg_kernel(const uint16_t* __restrict__ x, const float* __restrict__ wt,
-                                                         float* __restrict__ seg, int R, int K, int E)
+// large path, 1: segment sums seg[s][r][e] for a 128-row x 16 TE-expert tile of one segment, 8 x TE outputs per
+// thread (thread (ty, tx) of 16 x 16: rows 8 ty .., experts TE tx ..). A 32-k chunk of x (bf16 -> fp32) and of w is staged in
+// LDS k-major, so a thread reads its 8 rows and its 8 experts of one k as two 32-byte runs; the next chunk's global
+// loads are in flight while this chunk computes (two LDS buffers, one barrier per chunk). Per output: per chunk a
+// fmaf chain over k ascending from 0, the chunk totals added in order from 0 (the order of the small path).
+constexpr int SG_R = 128;
+template <int TE>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) router_seg_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ wt, float* __restrict__ seg, int R, int K, int E)
 {
-    __shared__ float xs[64][RCHUNK + 1];
-    __shared__ float ws[64][RCHUNK + 1];
-    const int r0 = blockIdx.x * 64, e0 = blockIdx.y * 64, s = blockIdx.z;
+    constexpr int SG_E = 16 * TE, WJ = 4 * TE / 8;      // experts per tile; w loads per thread per chunk
+    static_assert(TE == 4 || TE == 8, "4 or 8 experts per thread");
+    __shared__ __attribute__((aligned(16))) float xs[2][RCHUNK][SG_R];
+    __shared__ __attribute__((aligned(16))) float ws[2][RCHUNK][SG_E];
+    const int r0 = blockIdx.x * SG_R, e0 = blockIdx.y * SG_E, s = blockIdx.z;
     const int t = threadIdx.x, ty = t >> 4, tx = t & 15;
-    const int segk = K / RSEG, k0 = s * segk;
-    float acc[4][4], tot[4][4];
-    #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    const int segk = K / RSEG, k0 = s * segk, nch = segk / RCHUNK;
+    // staging: thread t loads row t % 128 of the tile, k 8 h .. + 8 for h = t / 128 and h + 2, and expert t % SG_E,
+    // k 4 h .. + 4 for h = t / SG_E + (256 / SG_E) j, j < WJ (rows / experts past the end load row 0 and stage zeros)
+    const int sr = t & 127, sh = t >> 7, se = t % SG_E, seh = t / SG_E;
+    const bool xin = r0 + sr < R, win = e0 + se < E;
+    const uint16_t* xp = x + (size_t) (xin ? r0 + sr : 0) * K + k0;
+    const float* wp = wt + (size_t) (win ? e0 + se : 0) * K + k0;
+    u32x4 gx[2];
+    f32x4 gw[WJ];
+    auto load = [&](int c) {
         #pragma unroll
-        for (int j = 0; j < 4; ++j) { acc[i][j] = 0.f; tot[i][j] = 0.f; }
-    for (int c = k0; c < k0 + segk; c += RCHUNK)
+        for (int h = 0; h < 2; ++h) gx[h] = *(const u32x4*) (xp + c * RCHUNK + 8 * (sh + 2 * h));
+        #pragma unroll
+        for (int j = 0; j < WJ; ++j) gw[j] = *(const f32x4*) (wp + c * RCHUNK + 4 * (seh + (256 / SG_E) * j));
+    };
+    auto store = [&](int b) {
+        #pragma unroll
+        for (int h = 0; h < 2; ++h)
+            #pragma unroll
+            for (int q = 0; q < 4; ++q)
+            {
+                const int k = 8 * (sh + 2 * h) + 2 * q;
+                xs[b][k][sr] = xin ? __uint_as_float(gx[h][q] << 16) : 0.f;
+                xs[b][k + 1][sr] = xin ? __uint_as_float(gx[h][q] & 0xffff0000u) : 0.f;
+            }
+        #pragma unroll
+        for (int j = 0; j < WJ; ++j)
+            #pragma unroll
+            for (int q = 0; q < 4; ++q) ws[b][4 * (seh + (256 / SG_E) * j) + q][se] = win ? gw[j][q] : 0.f;
+    };
+    float acc[8][TE], tot[8][TE];
+    #pragma unroll
+    for (int i = 0; i < 8; ++i)
+        #pragma unroll
+        for (int j = 0; j < TE; ++j) tot[i][j] = 0.f;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int c = 0; c < nch; ++c)
     {
-        // stage 64 x 32 of x (bf16 -> fp32) and of w: 2048 values each, 8 per thread
-        {
-            const int rr = t >> 2, kk = (t & 3) * 8;
-            const int gr = r0 + rr, ge = e0 + rr;
-            if (gr < R)
-            {
-                const u32x4 v = *(const u32x4*) (x + (size_t) gr * K + c + kk);
-                #pragma unroll
-                for (int q = 0; q < 4; ++q) { xs[rr][kk + 2 * q] = __uint_as_float(v[q] << 16); xs[rr][kk + 2 * q + 1] = __uint_as_float(v[q] & 0xffff0000u); }
-            }
-            else
-            {
-                #pragma unroll
-                for (int q = 0; q < 8; ++q) xs[rr][kk + q] = 0.f;
-            }
-            if (ge < E)
-            {
-                const f32x4 a = *(const f32x4*) (wt + (size_t) ge * K + c + kk), b = *(const f32x4*) (wt + (size_t) ge * K + c + kk + 4);
-                #pragma unroll
-                for (int q = 0; q < 4; ++q) { ws[rr][kk + q] = a[q]; ws[rr][kk + 4 + q] = b[q]; }
-            }
-            else
-            {
-                #pragma unroll
-                for (int q = 0; q < 8; ++q) ws[rr][kk + q] = 0.f;
-            }
-        }
-        __syncthreads();
-        #pragma unroll 8
+        const int b = c & 1;
+        if (c + 1 < nch) load(c + 1);
+        #pragma unroll
+        for (int i = 0; i < 8; ++i)
+            #pragma unroll
+            for (int j = 0; j < TE; ++j) acc[i][j] = 0.f;
+        #pragma unroll 4
         for (int k = 0; k < RCHUNK; ++k)
         {
-            float xv[4], wv[4];
+            const f32x4 xa = *(const f32x4*) &xs[b][k][8 * ty], xb = *(const f32x4*) &xs[b][k][8 * ty + 4];
+            float xv[8] = {xa[0], xa[1], xa[2], xa[3], xb[0], xb[1], xb[2], xb[3]}, wv[TE];
             #pragma unroll
-            for (int i = 0; i < 4; ++i) { xv[i] = xs[ty + 16 * i][k]; wv[i] = ws[tx + 16 * i][k]; }
-            #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int j = 0; j < TE; j += 4)
+            {
+                const f32x4 wq = *(const f32x4*) &ws[b][k][TE * tx + j];
                 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(xv[i], wv[j], acc[i][j]);
+                for (int q = 0; q < 4; ++q) wv[j + q] = wq[q];
+            }
+            #pragma unroll
+            for (int i = 0; i < 8; ++i)
+                #pragma unroll
+                for (int j = 0; j < TE; ++j) acc[i][j] = __builtin_fmaf(xv[i], wv[j], acc[i][j]);
         }
         #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 8; ++i)
             #pragma unroll
-            for (int j = 0; j < 4; ++j) { tot[i][j] = tot[i][j] + acc[i][j]; acc[i][j] = 0.f; }
+            for (int j = 0; j < TE; ++j) tot[i][j] = tot[i][j] + acc[i][j];
+        // the other buffer was last read in the previous chunk, before the barrier that ended it
+        if (c + 1 < nch) store(b ^ 1);
         __syncthreads();
     }
     #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 8; ++i)
+    {
+        const int r = r0 + 8 * ty + i;
+        if (r >= R) break;
         #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < TE; ++j)
         {
-            const int r = r0 + ty + 16 * i, e = e0 + tx + 16 * j;
-            if (r < R && e < E) seg[((size_t) s * R + r) * RMAXE + e] = tot[i][j];
+            const int e = e0 + TE * tx + j;
+            if (e < E) seg[((size_t) s * R + r) * RMAXE + e] = tot[i][j];
         }
+    }
 }
 
 // large path, 2: fold the segments in order, select; one wave per row; optional f16 copy of x
@@ -180,8 +210,14 @@ extern "C" int hmoe_router_fused(const void* x, const float* wt, const float* bi
         router_select_small_kernel<<<1, 1024, 0, st>>>(logits, bias, R, E, topk, scale, sel, rw);
         return HMOE_LAUNCHED("router_fused");
     }
-    dim3 g((R + 63) / 64, (E + 63) / 64, RSEG);
-    router_seg_kernel<<<g, 256, 0, st>>>((const uint16_t*) x, wt, logits, R, K, E);
+    // 128 experts per workgroup from 4096 rows (the 8 x 8 tiles are faster at 8192 rows, -115 us); fewer rows take 64
+    // experts per workgroup, so that the grid still fills the CUs twice over
+    if (R >= 4096)
+        router_seg_kernel<8><<<dim3((R + SG_R - 1) / SG_R, (E + 127) / 128, RSEG), 256, 0, st>>>(
+            (const uint16_t*) x, wt, logits, R, K, E);
+    else
+        router_seg_kernel<4><<<dim3((R + SG_R - 1) / SG_R, (E + 63) / 64, RSEG), 256, 0, st>>>(
+            (const uint16_t*) x, wt, logits, R, K, E);
     router_select_kernel<<<(R + 3) / 4, 256, 0, st>>>(logits, bias, R, E, topk, scale, sel, rw, (const uint16_t*) x,
                                                       (_Float16*) xh, K);
     return HMOE_LAUNCHED("router_fused");

@@ -5,8 +5,9 @@
 // rows (the ordered combine adds them) or adds them into out.
 //
 // dgemm_kernel: D[n][m] = sum_k X[n][k] W[m][k] over row-major W [M][K] (one matrix, or gate and up as two) and X
-// [N][K]. Workgroup = 4 waves as 2 (m) x 2 (n) = 32 TM / NMAT output rows x 32 TN tokens; wave (wm, wn) holds TM
-// weight tiles (TM / NMAT of each matrix) x TN token tiles of 16 x 16 in its accumulators. K runs in stages of 64:
+// [N][K]. Workgroup = WM x WN waves (WM along the weight rows, WN along the tokens) = 16 WM TM / NMAT output rows x
+// 16 WN TN tokens; wave (wm, wn) holds TM weight tiles (TM / NMAT of each matrix) x TN token tiles of 16 x 16 in its
+// accumulators. K runs in stages of 64:
 // both operands of a stage go to LDS by direct global-to-LDS loads, in a ring of 3 stages issued two ahead, so the
 // one wait and barrier per stage find the stage long arrived. A stage holds each 8 rows' 128 bytes as a 1 KB block:
 // one load per block, lane l taking row l / 8's 16-byte chunk (l % 8) ^ (l / 8) (whole 128-byte lines from memory),
@@ -153,8 +154,9 @@ dgemm_kernel(
     }
 }
 
-// gate and up: workgroups of 128 act columns x 128 tokens (TM 8 = 4 gate + 4 up tiles, TN 4: I / 128 x T / 128, 256
-// workgroups at 2048 tokens, one per CU); down: 192 output rows x 128 tokens (TM 6, TN 4: 512 workgroups at 2048)
+// 8 waves, two per SIMD (measured against 2 x 2 waves of twice the tiles and 2 x 4: -1 % and -0.5 % of the prefill
+// chunk): gate and up, workgroups of 128 act columns x 128 tokens (TM 4 = 2 gate + 2 up tiles, TN 4: I / 128 x T / 128,
+// 256 workgroups at 2048 tokens, one per CU); down, 192 output rows x 128 tokens (TM 3, TN 4: 512 at 2048)
 constexpr int GU_TM = 4, GU_TN = 4, GU_WM = 4, GU_WN = 2;
 constexpr int DN_TM = 3, DN_TN = 4, DN_WM = 4, DN_WN = 2;
 
