@@ -226,7 +226,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
         // stores it at 16 l, so a fragment read (row l % 16, chunk 4 (k % 2) + l / 16 of k half k / 2) meets distinct
         // banks. Wave w stages tiles 2w and 2w + 1: lane l's source row in each row half; a pick past the block re-reads
         // a valid row (its output columns are never stored), a whole tile past the block reads one fixed 16 bytes.
-        const _Float16* src[2][2];
+        uint32_t src[2][2];                                     // byte offsets from xin
         #pragma unroll
         for (int h = 0; h < 2; ++h)
             #pragma unroll
@@ -242,7 +242,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                     srow = (unsigned) tk < (unsigned) T ? tk : 0;
                 }
                 else srow = off + b.p0 + (in ? pk : 0);
-                src[h][rh] = xin + (size_t) srow * K + (tin ? 8 * ((l & 7) ^ (l >> 3)) : 0);
+                src[h][rh] = (uint32_t) (((size_t) srow * K + (tin ? 8 * ((l & 7) ^ (l >> 3)) : 0)) * 2);
             }
         int fo[4];
         #pragma unroll
@@ -264,12 +264,13 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                     #pragma unroll
                     for (int rh = 0; rh < 2; ++rh)
                     {
-                        const _Float16* gp = src[h][rh] + (tin ? kg * 128 + 64 * kh : 0);
+                        const uint32_t gp = src[h][rh] + (tin ? (kg * 128 + 64 * kh) * 2 : 0);
                         const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t) (uintptr_t)
                             (__attribute__((address_space(3))) void*) (buf + (tt * 4 + kh * 2 + rh) * 64));
     #pragma clang diagnostic push
     #pragma clang diagnostic ignored "-Winline-asm"
-                        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(gp), "s"(lds) : "memory", "m0");
+                        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" :: "v"(gp), "s"(xin), "s"(lds)
+                                     : "memory", "m0");
     #pragma clang diagnostic pop
                     }
             }
@@ -294,8 +295,11 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
             for (int m = 0; m < NMAT; ++m)
                 #pragma unroll
                 for (int tt = 0; tt < NTT; ++tt) acc[st][m][tt] = (f32x4) {0.f, 0.f, 0.f, 0.f};
+        // the prologue stages group 0 and fills D - 1 ring slots; group kg then issues its loads (the next stage and
+        // the refill of the slot group kg - 1 used, D - 1 groups ahead) only after its own operands are in hand, so
+        // that no wait for them counts the new loads: a weight refill has D - 1 groups to arrive
         stage(0, xs0);
-        static_for<D>([&](auto sc) {
+        static_for<D - 1>([&](auto sc) {
             fetch(decltype(sc)::value, sc);
             __builtin_amdgcn_sched_barrier(0);                  // keep the ring's issue order (waits count in order)
         });
@@ -306,13 +310,17 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                 const int kg = kg0 + s;
                 const bool even = (kg & 1) == 0;
                 u32x4* cur = even ? xs0 : xs1;
-                // this wave's staged loads of group kg are older than the FETCH_LOADS of the last refill (or, for kg = 0,
-                // than the D prologue refills); the barrier then makes every wave's group kg visible
-                if (kg == 0) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(FETCH_LOADS * D) : "memory");
+                // this wave's staged loads of group kg are older than the FETCH_LOADS of the refill issued with them
+                // (or, for kg = 0, than the D - 2 prologue refills after slot 0); the barrier then makes every wave's
+                // group kg visible
+                if (kg == 0) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(FETCH_LOADS * (D - 2)) : "memory");
                 else asm volatile("s_waitcnt vmcnt(%0)" :: "n"(FETCH_LOADS) : "memory");
                 __syncthreads();
-                if (kg + 1 < KG) stage(kg + 1, even ? xs1 : xs0);
+                // the slot's scales and first k step: the compiler's wait for the slot falls here, before the loads
+                // below (its count of later loads is then the D - 2 refills it knows of, and the stage, which has
+                // arrived, is the only load it does not count)
                 f16x2 sh[NS][NMAT];
+                f16x8 a0[NS][NMAT];
                 #pragma unroll
                 for (int st = 0; st < NS; ++st)
                     #pragma unroll
@@ -320,7 +328,12 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                     {
                         const _Float16 h = (_Float16) bf2f(ring[s].s[st][m]);
                         sh[st][m] = (f16x2) {h, h};
+                        a0[st][m] = dq8s(ring[s].q[st][m][0], sh[st][m], dq);
                     }
+                __builtin_amdgcn_sched_barrier(0);
+                if (kg + 1 < KG) stage(kg + 1, even ? xs1 : xs0);
+                fetch(min(kg + D - 1, KG - 1), std::integral_constant<int, (s + D - 1) % D>{});
+                __builtin_amdgcn_sched_barrier(0);
                 #pragma unroll
                 for (int k = 0; k < 4; ++k)
                 {
@@ -329,7 +342,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                     for (int st = 0; st < NS; ++st)
                         #pragma unroll
                         for (int m = 0; m < NMAT; ++m)
-                            a[st][m] = dq8s(ring[s].q[st][m][k], sh[st][m], dq);
+                            a[st][m] = k == 0 ? a0[st][m] : dq8s(ring[s].q[st][m][k], sh[st][m], dq);
                     // The pick tiles are read PD tiles ahead of their MFMAs (a tile past the block reads stale LDS
                     // data, never used). Each read is consumed by an empty asm after the MFMAs of the tile before it,
                     // which keeps the read ahead of the branch that ends the block's tiles: the compiler would
@@ -356,7 +369,6 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                         for (int i = 0; i < PD; ++i) bq[i] = bq[i + 1];
                     }
                 }
-                fetch(min(kg + D, KG - 1), sc);                 // refill the slot just used (clamped at the end)
             });
         }
         // epilogue: lane holds output rows 4(l/16)..+4 of pick tt*16 + l%16
@@ -514,6 +526,9 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
     HMOE_REQUIRE(x && tok && wt && rbt && ar && d && out, "moe4p_forward: null buffer");
     HMOE_REQUIRE(npos >= 0 && nrb >= 0 && npos <= ps && T >= 1 && topk >= 1 && topk <= TOPK,
                  "moe4p_forward: npos %d nrb %d ps %d T %d topk %d", npos, nrb, ps, T, topk);
+    // (the grouped GEMMs address their input rows by 32-bit byte offsets)
+    HMOE_REQUIRE((size_t) T * H * 2 <= UINT32_MAX && (size_t) (ps + T) * I * 2 <= UINT32_MAX,
+                 "moe4p_forward: T %d ps %d past the 4 GB input offsets", T, ps);
     HMOE_REQUIRE(n_tab >= 0 && n_tab <= HMOE_MAXE && (n_tab == 0 || (gw && uw && dw && gs && us && ds)),
                  "moe4p_forward: tables");
     HMOE_REQUIRE((!sh_gw && !sh_uw && !sh_dw) || (sh_gw && sh_uw && sh_dw && inv),
@@ -622,6 +637,8 @@ extern "C" int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid,
     HMOE_REQUIRE(x && tok && wt && rbt && ar && out, "moe4t_forward: null buffer");
     HMOE_REQUIRE(npos > 0 && nrb >= 0 && npos <= ps && T >= 1, "moe4t_forward: npos %d nrb %d ps %d T %d", npos, nrb, ps,
                  T);
+    HMOE_REQUIRE((size_t) T * H * 2 <= UINT32_MAX && (size_t) ps * I * 2 <= UINT32_MAX,
+                 "moe4t_forward: T %d ps %d past the 4 GB input offsets", T, ps);
     HMOE_REQUIRE(n_tab >= 1 && n_tab <= HMOE_MAXE && gw && uw && dw && gs && us && ds, "moe4t_forward: tables");
     HMOE_REQUIRE(xf == HMOE_XF_BF16 || xf == HMOE_XF_F16, "moe4t_forward: xf must be HMOE_XF_BF16 (0) or HMOE_XF_F16 (2)");
     HMOE_REQUIRE(((uintptr_t) x & 15) == 0 && ((uintptr_t) ar & 15) == 0 && ((uintptr_t) out & 15) == 0 &&
@@ -662,6 +679,8 @@ extern "C" int hmoe_moe4t_gemm(const void* xs, int rows, const int* rbt, int nrb
     HMOE_REQUIRE(xs && rbt && out && w0 && s0 && (down || (w1 && s1)), "moe4t_gemm: null buffer");
     HMOE_REQUIRE(rows >= 1 && nrb >= 0 && ps >= rows && n_tab >= 1 && n_tab <= HMOE_MAXE,
                  "moe4t_gemm: rows %d nrb %d ps %d n_tab %d", rows, nrb, ps, n_tab);
+    HMOE_REQUIRE((size_t) rows * (down ? I : H) * 2 <= UINT32_MAX, "moe4t_gemm: rows %d past the 4 GB input offsets",
+                 rows);
     HMOE_REQUIRE(((uintptr_t) xs & 15) == 0 && ((uintptr_t) out & 15) == 0, "moe4t_gemm: alignment");
     if (nrb == 0) return HMOE_OK;
     hipStream_t st = (hipStream_t) stream;
