@@ -161,7 +161,8 @@ __device__ __forceinline__ bool get_block(const int* rbt, int nrb, const int* me
 //   * the block's input rows are staged in LDS as f16 by direct global-to-LDS loads (double-buffered, one barrier
 //     per group): the next group's rows load while this group computes;
 //   * the weight tiles come from a ring of D groups of unconditional 16-byte loads (and the lane's row scale), issued
-//     D groups ahead, so HBM latency hides behind D groups of MFMA work; each tile is loaded once per workgroup;
+//     D - 1 groups ahead, so HBM latency hides behind that many groups of MFMA work; each tile is loaded once per
+//     workgroup;
 //   * each k step dequantises the 4 weight fragments (exact f16 codes times the f16 group scale) and runs the
 //     16x16x32 MFMA against the block's 16-pick tiles (up to 8).
 template <int NMAT, int NS>
