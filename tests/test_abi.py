@@ -244,3 +244,18 @@ def test_moe4t_no_picks_is_a_no_op():
     assert L.hmoe_moe4t_scratch_bytes(1, 100) == 100 * 2048 * 2
     assert L.hmoe_moe4t_scratch_bytes(2, 100) == 100 * 6144 * 4
     assert L.hmoe_shared_forward(None, 0, None, None, None, None, None, 0, None) == 0
+
+
+def test_prefill_chunks_past_the_32_bit_offsets_are_refused():
+    """the grouped GEMMs address their input rows by 32-bit byte offsets: a chunk whose f16 x (T x 6144) or act rows
+    ((ps + T) x 2048) pass 4 GB is refused before any launch, here and through moe4t and the test entry"""
+    L = _lib.lib()
+    b = _fake()
+    p = b.ctypes.data
+    big = 400_000                                                           # 400,000 x 6144 x 2 B > 4 GB
+    pf = lambda T, ps: [p, p, p, p, p, 8, 1, 8] + [p] * 10 + [ps, None, None, T, 8, None, None, None, _lib.XF_BF16, None]
+    assert L.hmoe_moe4p_forward(*pf(big, 8)) == 1 and b"4 GB" in L.hmoe_last_error()
+    assert L.hmoe_moe4p_forward(*pf(8, 1_100_000)) == 1 and b"4 GB" in L.hmoe_last_error()
+    assert L.hmoe_moe4t_forward(p, p, p, p, p, 8, 1, 8, *([p] * 10), 8, None, big, _lib.XF_BF16, None, 8, None) == 1
+    assert b"4 GB" in L.hmoe_last_error()
+    assert L.hmoe_moe4t_gemm(p, big, p, 1, 8, p, p, p, p, p, big, 0, None) == 1 and b"4 GB" in L.hmoe_last_error()
