@@ -88,6 +88,27 @@ def test_router_bit_exact(dev, R, bias_sigma):
     assert np.array_equal(u16(xh), O.f32_to_f16(O.bf16_to_f32(x)))
 
 
+@pytest.mark.parametrize("R,E", [(300, 160), (4100, 200)])
+def test_router_large_path_partial_tiles(dev, R, E):
+    """the large path's segment GEMM on partial tiles: 300 rows (128-row tiles, 64 experts per workgroup) and 4100 rows
+    (128 experts per workgroup) with fewer experts than a whole tile covers; logits, selection and weights bit-exact
+    with the oracle's fixed order"""
+    log(f"router large path R={R} E={E}")
+    rng = np.random.default_rng(R + E)
+    x = x_rows(7 + R, R)
+    wg = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.001).astype(np.float32)
+    lg_ref = O.router_logits(x, wg)
+    sel_ref, rw_ref = O.router_select(lg_ref, bias)
+    xt = torch.from_numpy(x.view(np.int16)).to(dev).view(torch.bfloat16)
+    logits, ctr = router.buffers(R, dev)
+    sel = torch.empty((R, 8), dtype=torch.int64, device=dev); rw = torch.empty((R, 8), dtype=torch.float16, device=dev)
+    router.router_fused(xt, torch.from_numpy(wg).to(dev), torch.from_numpy(bias).to(dev), logits, ctr, sel, rw, 8, 2.5)
+    torch.cuda.synchronize()
+    assert np.array_equal(sel.cpu().numpy(), sel_ref)
+    assert np.array_equal(u16(rw), rw_ref)
+
+
 @pytest.mark.parametrize("R", [4, 20])
 def test_router_forced_tie_lowest_index(dev, R):
     """the forced tie of the oracle's test at the top-8 boundary through both router paths (R <= 16, R > 16): an
