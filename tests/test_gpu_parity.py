@@ -579,7 +579,7 @@ def test_prefill_blocks_of_256_picks(dev):
     del pb
 
 
-@pytest.mark.parametrize("T,ordered", [(4096, False), (4096, True), (8192, True)])
+@pytest.mark.parametrize("T,ordered", [(2049, True), (4096, False), (4096, True), (8192, True)])
 def test_long_prefill_moe4t(dev, T, ordered):
     """chunks above 2048 rows on moe4t (tier_split.py:543): 256-pick balanced blocks, the shared expert apart; the
     combine either in the down GEMM's epilogue (fp32 atomics, as the reference) or ordered per token through the
