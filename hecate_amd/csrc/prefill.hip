@@ -146,12 +146,14 @@ __device__ __forceinline__ void xcd_tile(int& rb, int& cb)
 
 static dim3 pgemm_grid(int nrb, int ny) { return dim3((nrb + 7) & ~7, ny); }
 
-// row block rb of the plan: up to 2 PB picks (the dispatch's bm <= 256), run as halves of <= PB picks
-__device__ __forceinline__ bool get_block(const int* rbt, int nrb, const int* meta, int n_tab, int rb, Block& b)
+// row block rb of the plan: up to 2 PB picks (the dispatch's bm <= 256), run as halves of <= PB picks; a block
+// whose expert or picks fall outside the tables (np picks) is skipped, so a caller's malformed plan reads nothing
+// out of bounds
+__device__ __forceinline__ bool get_block(const int* rbt, int nrb, const int* meta, int n_tab, int np, int rb, Block& b)
 {
     if (rb >= nrb || (meta && rb >= meta[1])) return false;
     b.e = rbt[4 * rb]; b.p0 = rbt[4 * rb + 1]; b.rows = min(rbt[4 * rb + 2], 2 * PB);
-    return b.e >= 0 && b.e < n_tab && b.rows > 0;
+    return b.e >= 0 && b.e < n_tab && b.rows > 0 && b.p0 >= 0 && b.p0 <= np - b.rows;
 }
 
 // A pipelined grouped GEMM for both projections. Workgroup = (row block of <= 128 picks of one expert, 64 NS output
@@ -183,7 +185,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
     const _Float16* __restrict__ xin, const int* __restrict__ tok, const float* __restrict__ wt,
     const int* __restrict__ rbt, int nrb, const int* __restrict__ meta, int n_tab,
     const int64_t* __restrict__ w0, const int64_t* __restrict__ w1, const int64_t* __restrict__ s0,
-    const int64_t* __restrict__ s1, _Float16* __restrict__ ar, float* __restrict__ dout, int T, int off,
+    const int64_t* __restrict__ s1, _Float16* __restrict__ ar, float* __restrict__ dout, int T, int off, int np,
     float* __restrict__ fout = nullptr, int ps = 0)
 {
     static_assert((NMAT == 2) == (EPI == EPI_ACT || EPI == EPI_RAW), "gate/up epilogues need both matrices");
@@ -201,7 +203,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
     int rbi, cbi;
     xcd_tile(rbi, cbi);
     Block rb;
-    if (!get_block(rbt, nrb, meta, n_tab, rbi, rb)) return;
+    if (!get_block(rbt, nrb, meta, n_tab, np, rbi, rb)) return;
     // a block of more than PBX picks runs as passes of PBX, one after the other (a later pass reads the weights
     // again, mostly from the caches); the barrier between them keeps one pass's last LDS reads ahead of the next
     // pass's first staging
@@ -552,13 +554,13 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
     if (nrb > 0)
     {
         pgemm_kernel<2, 2, 2><<<pgemm_grid(nrb, I / 128), PT, 0, st>>>((const _Float16*) xb, tok, wt, rbt, nrb, meta,
-            n_tab, gw, uw, gs, us, a, nullptr, T, 0);
+            n_tab, gw, uw, gs, us, a, nullptr, T, 0, npos);
         if (inv)
             pgemm_kernel<1, 4, 2><<<pgemm_grid(nrb, H / 256), PT, 0, st>>>(a, nullptr, nullptr, rbt, nrb, meta, n_tab, dw,
-                nullptr, ds, nullptr, nullptr, d, T, 0);
+                nullptr, ds, nullptr, nullptr, d, T, 0, npos);
         else
             pgemm_kernel<1, 4, 2, EPI_FIN><<<pgemm_grid(nrb, H / 256), PT, 0, st>>>(a, tok, nullptr, rbt, nrb, meta, n_tab,
-                dw, nullptr, ds, nullptr, nullptr, nullptr, T, 0, out);
+                dw, nullptr, ds, nullptr, nullptr, nullptr, T, 0, npos, out);
     }
     const bool sh = sh_gw != nullptr;
     if (sh)
@@ -660,14 +662,14 @@ extern "C" int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid,
         // 256-pick blocks in one pass: 8 waves, each one 16-row strip of gate and of up (or two of down) against the
         // block's 16 pick tiles
         pgemm_kernel<2, 1, 4, EPI_ACT, 16, 8><<<pgemm_grid(nrb, I / 128), 512, 0, st>>>(xh, tok, wt, rbt, nrb, meta, n_tab,
-            gw, uw, gs, us, (_Float16*) ar, nullptr, T, 0);
+            gw, uw, gs, us, (_Float16*) ar, nullptr, T, 0, npos);
         // (d held the f16 copy of x, which the gate/up GEMM has consumed by now: the down rows may overwrite it)
         if (inv)
             pgemm_kernel<1, 2, 4, EPI_D, 16, 8><<<pgemm_grid(nrb, H / 256), 512, 0, st>>>((const _Float16*) ar, nullptr,
-                nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, d, T, 0);
+                nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, d, T, 0, npos);
         else
             pgemm_kernel<1, 2, 4, EPI_FIN, 16, 8><<<pgemm_grid(nrb, H / 256), 512, 0, st>>>((const _Float16*) ar, tok,
-                nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, nullptr, T, 0, out);
+                nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, nullptr, T, 0, npos, out);
     }
     if (inv) pfin_kernel<<<T, 256, 0, st>>>(d, inv, topk, -1, out);
     return HMOE_LAUNCHED("moe4t_forward");
@@ -687,9 +689,9 @@ extern "C" int hmoe_moe4t_gemm(const void* xs, int rows, const int* rbt, int nrb
     hipStream_t st = (hipStream_t) stream;
     if (down)
         pgemm_kernel<1, 4, 2><<<pgemm_grid(nrb, H / 256), PT, 0, st>>>((const _Float16*) xs, nullptr, nullptr, rbt, nrb,
-            nullptr, n_tab, w0, nullptr, s0, nullptr, nullptr, out, rows, 0);
+            nullptr, n_tab, w0, nullptr, s0, nullptr, nullptr, out, rows, 0, rows);
     else
         pgemm_kernel<2, 2, 2, EPI_RAW><<<pgemm_grid(nrb, I / 128), PT, 0, st>>>((const _Float16*) xs, nullptr, nullptr,
-            rbt, nrb, nullptr, n_tab, w0, w1, s0, s1, nullptr, out, rows, 0, nullptr, ps);
+            rbt, nrb, nullptr, n_tab, w0, w1, s0, s1, nullptr, out, rows, 0, rows, nullptr, ps);
     return HMOE_LAUNCHED("moe4t_gemm");
 }
