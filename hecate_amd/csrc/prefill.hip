@@ -436,7 +436,7 @@ __global__ void __launch_bounds__(256) to_f16_kernel(const uint16_t* __restrict_
 // load is unconditional (an absent pick or shared row reads row 0 and is dropped by a select at its add), so all of
 // them are in flight together: under a branch each load was followed by a wait for it.
 __global__ void __launch_bounds__(256) pfin_kernel(const float* __restrict__ d, const int* __restrict__ inv, int topk,
-                                                   int sh_off, float* __restrict__ out)
+                                                   int np, int sh_off, float* __restrict__ out)
 {
     constexpr int NR = HMOE_TOPK + 1;
     const int t = blockIdx.x;
@@ -446,8 +446,8 @@ __global__ void __launch_bounds__(256) pfin_kernel(const float* __restrict__ d, 
     for (int k = 0; k < HMOE_TOPK; ++k)
     {
         const int p = k < topk ? inv[(size_t) t * topk + min(k, topk - 1)] : -1;
-        use[k] = p >= 0;
-        pos[k] = max(p, 0);
+        use[k] = (unsigned) p < (unsigned) np;                      // -1: a pick outside the window
+        pos[k] = use[k] ? p : 0;
     }
     use[HMOE_TOPK] = sh_off >= 0;
     pos[HMOE_TOPK] = sh_off >= 0 ? sh_off + t : 0;
@@ -573,7 +573,7 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
         if (int rc = dense_down((const _Float16*) sh_dw, a + (size_t) ps * I, T, d + (size_t) ps * H, false, st))
             return rc;
     }
-    if (inv) pfin_kernel<<<T, 256, 0, st>>>(d, inv, topk, sh ? ps : -1, out);
+    if (inv) pfin_kernel<<<T, 256, 0, st>>>(d, inv, topk, npos, sh ? ps : -1, out);
     return HMOE_LAUNCHED("moe4p_forward");
 }
 
@@ -671,7 +671,7 @@ extern "C" int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid,
             pgemm_kernel<1, 2, 4, EPI_FIN, 16, 8><<<pgemm_grid(nrb, H / 256), 512, 0, st>>>((const _Float16*) ar, tok,
                 nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, nullptr, T, 0, npos, out);
     }
-    if (inv) pfin_kernel<<<T, 256, 0, st>>>(d, inv, topk, -1, out);
+    if (inv) pfin_kernel<<<T, 256, 0, st>>>(d, inv, topk, npos, -1, out);
     return HMOE_LAUNCHED("moe4t_forward");
 }
 
