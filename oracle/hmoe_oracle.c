@@ -295,6 +295,20 @@ static void gemv_i4_q8(const uint8_t* q, const uint16_t* s, int N, int K, const 
     }
 }
 
+/* the q8_0 primitives on their own, for the oracle's tests: every row of x [nr][K] quantised per 32 (quant_group),
+ * then y[r][n] = gemv_i4_q8 over packed codes q [N][K/2] (low nibble = even k) and bf16 group scales s [N][K/128];
+ * xq / xg receive the quantised rows and their group scales */
+int orc_q8_gemv(const uint8_t* q, const uint16_t* s, int N, int K, const float* x, int nr, int8_t* xq, float* xg,
+                float* y)
+{
+    if (nr < 1 || nr > 16 || K % 128 != 0) return -1;
+    for (int r = 0; r < nr; ++r)
+        for (int g = 0; g < K / 32; ++g)
+            quant_group(x + (size_t) r * K + g * 32, xq + (size_t) r * K + g * 32, xg + (size_t) r * (K / 32) + g);
+    gemv_i4_q8(q, s, N, K, xq, xg, nr, y, N, 1);
+    return 0;
+}
+
 /* fp32 dense GEMV of the shared expert in the q8 mode (the adaptation named for the CPU baseline) */
 static void gemv_bf16_f32(const uint16_t* w, int N, int K, const float* x, int nr, size_t xstride, float* y,
                           size_t ystride, int threads)

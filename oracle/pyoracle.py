@@ -42,6 +42,7 @@ def lib():
             "orc_pick_groups": (i32, [P, i32, i32, i32, P, i32]),
             "orc_picks": (i32, [P, P, i32, i32, i32, i32, P, P]),
             "orc_moe": (i32, [i32, i32, i32, i32, P, P, P, i32, i32, i32, P, P, P, P, P, P, P, P, P, i32, P, i32]),
+            "orc_q8_gemv": (i32, [P, P, i32, i32, P, i32, P, P, P]),
             "orc_dequant": (None, [P, P, i32, i32, P]),
             "orc_residual_rmsnorm": (None, [P, P, P, i32, i32, f32, P]),
         }
@@ -187,6 +188,16 @@ class ExpertTable:
                 if ex is not None:
                     t[i] = ex[name].ctypes.data
             self.tabs[name] = t
+
+
+def q8_gemv(q, s, x):
+    """orc_q8_gemv: x fp32 [nr][K] quantised per 32 (q8_0), times packed codes q [N][K/2] with bf16 group scales
+    s [N][K/128]; returns (y [nr][N], xq int8 [nr][K], xg [nr][K/32])"""
+    q = _c(q, np.uint8); s = _c(s, np.uint16); x = _c(x, np.float32)
+    N = q.shape[0]; nr, K = x.shape
+    xq = np.empty((nr, K), np.int8); xg = np.empty((nr, K // 32), np.float32); y = np.empty((nr, N), np.float32)
+    assert lib().orc_q8_gemv(_p(q), _p(s), N, K, _p(x), nr, _p(xq), _p(xg), _p(y)) == 0
+    return y, xq, xg
 
 
 def moe(mode, x_bf16, sel, rw, table, lo, n_hot, shared=None, out=None, accumulate=False, threads=8, H=6144, I=2048):

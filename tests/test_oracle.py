@@ -378,3 +378,49 @@ def test_bf16_ulp_is_the_spacing_of_bf16():
     up = (b & 0x8000) | ((b & 0x7fff) + 1)                     # next magnitude (sign kept)
     spacing = np.abs(O.bf16_to_f32(up).astype(np.float64) - O.bf16_to_f32(b).astype(np.float64))
     assert np.array_equal(bf16_ulp(O.bf16_to_f32(b)), spacing)
+
+
+def test_q8_quantisation_and_integer_dot_in_closed_form():
+    """cpuband.cpp:106-111 and :80-104 on values where every step is exact: each 32-block's absmax is 127 * 2^e, so
+    its scale absmax / 127 is a power of two and v / s lands on chosen integers and half-integers; the weights' group
+    scales are powers of two and the integer sums stay below 2^24, so the fp32 result equals the closed form
+    s_w * sum over blocks of s_x * sum q * (code - 8) exactly. The half-integer cases tell round-half-to-even
+    (lrintf in the default mode: 64.5 -> 64, 63.5 -> 64, -64.5 -> -64, 0.5 -> 0, 2.5 -> 2) from truncation and
+    from rounding half away from zero, and the codes differ between neighbouring k, so the nibble order (even k in
+    the low nibble) and the scale's divisor (127, not 128) are pinned as well"""
+    rng = np.random.default_rng(41)
+    N, K, nr = 5, 256, 2
+    exps = rng.integers(-6, 2, size=(nr, K // 32))
+    qx = rng.integers(-126, 127, size=(nr, K)).astype(np.float64)          # v / s before the ties are planted
+    ties = np.array([64.5, 63.5, -64.5, 0.5, 1.5, 2.5, -2.5, -0.5])
+    for r in range(nr):
+        for b in range(K // 32):
+            blk = qx[r, 32 * b: 32 * b + 32]
+            blk[0] = 127.0 if (r + b) % 2 == 0 else -127.0                  # the absmax
+            blk[1:1 + len(ties)] = ties
+    x = (qx * np.exp2(np.repeat(exps, 32, axis=1))).astype(np.float32)     # exact in fp32
+    codes = rng.integers(0, 16, size=(N, K)).astype(np.uint8)
+    codes[:, 1::2] = (codes[:, 0::2] + 1 + rng.integers(0, 14, size=(N, K // 2))) % 16   # neighbours differ
+    packed = np.ascontiguousarray(codes[:, 0::2] | (codes[:, 1::2] << 4))
+    sexp = rng.integers(-9, -5, size=(N, K // 128))
+    scales = O.f32_to_bf16(np.exp2(sexp).astype(np.float32))
+    y, xq, xg = O.q8_gemv(packed, scales, x)
+    q_exp = np.where(np.abs(qx - np.trunc(qx)) == 0.5, 2.0 * np.round(qx / 2.0), np.round(qx)).astype(np.int64)
+    assert np.array_equal(q_exp[:, 1:9], np.array([[64, 64, -64, 0, 2, 2, -2, 0]] * nr))
+    assert np.array_equal(xq.astype(np.int64), q_exp)
+    assert np.array_equal(xg, np.exp2(exps).astype(np.float32))
+    w = codes.astype(np.int64) - 8
+    ref = np.zeros((nr, N))
+    for r in range(nr):
+        for n in range(N):
+            for g in range(K // 128):
+                acc = 0.0
+                for b in range(4 * g, 4 * g + 4):
+                    acc += float(np.exp2(exps[r, b])) * float(np.dot(q_exp[r, 32 * b: 32 * b + 32], w[n, 32 * b: 32 * b + 32]))
+                ref[r, n] += float(np.exp2(sexp[n, g])) * acc
+    assert np.array_equal(y.astype(np.float64), ref)
+    # the case has the power to see a swapped nibble order or a /128 scale
+    swapped = codes.copy(); swapped[:, 0::2], swapped[:, 1::2] = codes[:, 1::2], codes[:, 0::2]
+    y_sw, _, _ = O.q8_gemv(np.ascontiguousarray(swapped[:, 0::2] | (swapped[:, 1::2] << 4)), scales, x)
+    assert not np.array_equal(y_sw, y)
+    assert not np.array_equal(np.round(qx * 127.0 / 128.0).astype(np.int64), q_exp)
