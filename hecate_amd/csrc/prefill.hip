@@ -162,16 +162,17 @@ __device__ __forceinline__ bool get_block(const int* rbt, int nrb, const int* me
 // 16-pick input fragment from LDS once for 4 MFMAs. Per 128-k group kg:
 //   * the block's input rows are staged in LDS as f16 by direct global-to-LDS loads (double-buffered, one barrier
 //     per group): the next group's rows load while this group computes;
-//   * the weight tiles come from a ring of D groups of unconditional 16-byte loads (and the lane's row scale), issued
-//     D - 1 groups ahead, so HBM latency hides behind that many groups of MFMA work; each tile is loaded once per
-//     workgroup;
+//   * the weight tiles come from a ring of D groups of unconditional 16-byte loads, issued D - 1 groups ahead, so HBM
+//     latency hides behind that many groups of MFMA work; each tile is loaded once per workgroup; the lane's row
+//     scales come 4 groups at a time (one 8-byte load per fragment every fourth group);
 //   * each k step dequantises the 4 weight fragments (exact f16 codes times the f16 group scale) and runs the
 //     16x16x32 MFMA against the block's 16-pick tiles (up to 8).
+// Every vector-memory instruction costs issue time on the SIMD beside the MFMA and dequantisation work, so the loads
+// are few and their addresses cheap: uniform bases in scalar registers with 32-bit lane offsets.
 template <int NMAT, int NS>
 struct PFetch
 {
     u32x4 q[NS][NMAT];
-    uint16_t s[NS][NMAT];
 };
 
 // epilogues: gate/up -> act f16 (EPI_ACT) or the raw gate and up sums (EPI_RAW, fp32 [2][ps][I], the test entry of
@@ -253,9 +254,8 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
             fo[k] = ((k >> 1) * 2 + (row >> 3)) * 64 + 8 * (l & 7) + ((4 * (k & 1) + (l >> 4)) ^ (l & 7));
         // Direct global-to-LDS loads (16 bytes per lane, lane l at LDS base + 16 l), issued from inline assembly: the
         // compiler then does not count them, so its own waits for the weight ring stay exact, and the wait that makes a
-        // staged group visible is placed by hand before the barrier (the loads issued after a stage are exactly the
-        // FETCH_LOADS of one ring refill). M0 holds the LDS base of each load; nothing else in this kernel uses M0.
-        constexpr int FETCH_LOADS = NS * NMAT * 2;
+        // staged group visible is placed by hand before the barrier (the loads issued after a stage are exactly those
+        // of one ring refill). M0 holds the LDS base of each load; nothing else in this kernel uses M0.
         auto stage = [&](int kg, u32x4* buf) {
             #pragma unroll
             for (int h = 0; h < 2; ++h)
@@ -279,16 +279,22 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
             }
         };
         PFetch<NMAT, NS> ring[D];
-        auto fetch = [&](int kg, auto sc) {
-            constexpr int s = decltype(sc)::value;
+        // the row scales of two blocks of 4 groups (a block's 4 bf16 of one row are 8 contiguous bytes of I4G128)
+        u32x2 sc4[2][NS][NMAT];
+        // the weights of group kg into ring slot SL; when kg starts a block of 4, the block's scales too, into sc4[SC]
+        // (SC = -1: none). Offsets are 32-bit (an expert's matrix is 6.3 MB), so the loads take the base from scalar
+        // registers.
+        auto fetch = [&](int kg, auto sl, auto sc) {
+            constexpr int SL = decltype(sl)::value, SC = decltype(sc)::value;
             #pragma unroll
             for (int st = 0; st < NS; ++st)
                 #pragma unroll
                 for (int m = 0; m < NMAT; ++m)
                 {
                     const int nb = nb0 + st;
-                    ring[s].q[st][m] = ldw16(wp[m] + ((size_t) (nb * KG + kg) * 64 + l) * 16);
-                    ring[s].s[st][m] = ldg<uint16_t>(sp[m] + sc_index(nb * 16 + row, kg, KG) * 2);
+                    ring[SL].q[st][m] = ldw16(wp[m] + (uint32_t) (((nb * KG + kg) * 64 + l) * 16));
+                    if constexpr (SC >= 0)
+                        sc4[SC][st][m] = ld8(sp[m] + (uint32_t) (sc_index(nb * 16 + row, kg & ~3, KG) * 2));
                 }
         };
         f32x4 acc[NS][NMAT][NTT];
@@ -303,21 +309,27 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
         // that no wait for them counts the new loads: a weight refill has D - 1 groups to arrive
         stage(0, xs0);
         static_for<D - 1>([&](auto sc) {
-            fetch(decltype(sc)::value, sc);
+            constexpr int g = decltype(sc)::value;
+            fetch(g, sc, std::integral_constant<int, g % 4 == 0 ? (g / 4) % 2 : -1>{});
             __builtin_amdgcn_sched_barrier(0);                  // keep the ring's issue order (waits count in order)
         });
-        for (int kg0 = 0; kg0 < KG; kg0 += D)
+        // the group loop runs in steps of 8, so that the ring slot (kg % D), the scale block (kg / 4 % 2) and whether a
+        // refill starts a block are compile-time constants
+        static_assert(KG % 8 == 0 && 8 % D == 0, "the group loop runs in steps of 8");
+        for (int kg0 = 0; kg0 < KG; kg0 += 8)
         {
-            static_for<D>([&](auto sc) {
-                constexpr int s = decltype(sc)::value;
-                const int kg = kg0 + s;
+            static_for<8>([&](auto sc8) {
+                constexpr int s8 = decltype(sc8)::value, s = s8 % D;
+                const int kg = kg0 + s8;
                 const bool even = (kg & 1) == 0;
                 u32x4* cur = even ? xs0 : xs1;
-                // this wave's staged loads of group kg are older than the FETCH_LOADS of the refill issued with them
-                // (or, for kg = 0, than the D - 2 prologue refills after slot 0); the barrier then makes every wave's
-                // group kg visible
-                if (kg == 0) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(FETCH_LOADS * (D - 2)) : "memory");
-                else asm volatile("s_waitcnt vmcnt(%0)" :: "n"(FETCH_LOADS) : "memory");
+                // this wave's staged loads of group kg are older than the loads of the refill issued with them in group
+                // kg - 1 (its NS NMAT weight loads and, when that refill started a block of 4, as many scale loads); for
+                // kg = 0 every load is waited for. The barrier then makes every wave's group kg visible.
+                constexpr int gp = (s8 + 7) % 8 + D - 1;            // the group refilled in group kg - 1, mod 8
+                constexpr int after = NS * NMAT * (gp % 4 == 0 ? 2 : 1);
+                if (kg == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                else asm volatile("s_waitcnt vmcnt(%0)" :: "n"(after) : "memory");
                 __syncthreads();
                 // the slot's scales and first k step: the compiler's wait for the slot falls here, before the loads
                 // below (its count of later loads is then the D - 2 refills it knows of, and the stage, which has
@@ -329,13 +341,19 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                     #pragma unroll
                     for (int m = 0; m < NMAT; ++m)
                     {
-                        const _Float16 h = (_Float16) bf2f(ring[s].s[st][m]);
+                        const uint32_t sw = sc4[s8 / 4][st][m][(s8 % 4) / 2];     // bf16 of group kg: half s8 % 2
+                        const _Float16 h = (_Float16) __uint_as_float(s8 % 2 == 0 ? sw << 16 : sw & 0xffff0000u);
                         sh[st][m] = (f16x2) {h, h};
                         a0[st][m] = dq8s(ring[s].q[st][m][0], sh[st][m], dq);
                     }
                 __builtin_amdgcn_sched_barrier(0);
                 if (kg + 1 < KG) stage(kg + 1, even ? xs1 : xs0);
-                fetch(min(kg + D - 1, KG - 1), std::integral_constant<int, (s + D - 1) % D>{});
+                // the refill: group kg + D - 1, clamped to the last group; it starts a block of 4 when (s8 + D - 1) % 4
+                // == 0, whose scales go to sc4[(s8 + D - 1) / 4 % 2] (kg0 is a multiple of 8). Past the last group the
+                // clamped group's block is loaded again into the buffer that no remaining group reads.
+                constexpr int gn = s8 + D - 1;
+                fetch(min(kg + D - 1, KG - 1), std::integral_constant<int, (s + D - 1) % D>{},
+                      std::integral_constant<int, gn % 4 == 0 ? (gn / 4) % 2 : -1>{});
                 __builtin_amdgcn_sched_barrier(0);
                 #pragma unroll
                 for (int k = 0; k < 4; ++k)
