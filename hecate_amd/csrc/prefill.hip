@@ -272,8 +272,9 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                             (__attribute__((address_space(3))) void*) (buf + (tt * 4 + kh * 2 + rh) * 64));
     #pragma clang diagnostic push
     #pragma clang diagnostic ignored "-Winline-asm"
-                        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" :: "v"(gp), "s"(xin), "s"(lds)
-                                     : "memory", "m0");
+                        // (an SALU write of M0 needs one wait state before an LDS-DMA load reads it: the s_nop)
+                        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" :: "v"(gp), "s"(xin),
+                                     "s"(lds) : "memory", "m0");
     #pragma clang diagnostic pop
                     }
             }

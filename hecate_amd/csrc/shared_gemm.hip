@@ -77,7 +77,8 @@ dgemm_kernel(
                 (uint32_t) (uintptr_t) (__attribute__((address_space(3))) void*) (buf + (w + NW * i) * 64));
     #pragma clang diagnostic push
     #pragma clang diagnostic ignored "-Winline-asm"
-            asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" :: "v"(v), "s"(base), "s"(la)
+            // (an SALU write of M0 needs one wait state before an LDS-DMA load reads it: the s_nop)
+            asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" :: "v"(v), "s"(base), "s"(la)
                          : "memory", "m0");
     #pragma clang diagnostic pop
         }
