@@ -48,12 +48,12 @@ constexpr int DW = 16;                     // down waves: slot w / 4 of the quad
 constexpr int MAX_PARTS = 1 + MAXSLOT / 4;
 constexpr int CTR_WORDS = 1024;            // ctr[0]: the part count of the last down launch
 
-struct Route
+struct __attribute__((aligned(16))) Route
 {
+    float w[MAXSLOT][MAXR];
     int m;
     unsigned mask[8];
     short e[MAXSLOT];
-    float w[MAXSLOT][MAXR];
 };
 
 // one pick (expert id, f16 routing weight) of the step
@@ -84,6 +84,60 @@ __device__ void route_picks(Pick pk, int R, int lo, int n_hot, Route& rt)
     }
     if (t == 0) { int m = 0; for (int wd = 0; wd < 8; ++wd) m += __popc(rt.mask[wd]); rt.m = m; }
     __syncthreads();
+}
+
+// lanes of one wave exchanging data through LDS: the stores before are done before the loads after. LDS operations of
+// one wave take effect in issue order; this keeps the compiler from moving a lane's load above another lane's store
+// (which a lane's own program order does not forbid).
+__device__ __forceinline__ void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// route_picks() for a selection in LDS (sel / rw, R rows of TOPK), done by wave 0 alone (it returns at once in the other
+// waves) and with no workgroup barrier: its phases (zeroing, ors, reads, results) are separated by wave_lds_sync(). Within one row the picks are distinct experts, so every (slot, row)
+// weight has at most one pick and is stored, not added. The caller's next barrier publishes rt.
+__device__ void route_wave(const int64_t* sel, const uint16_t* rw, int R, int lo, int n_hot, Route& rt)
+{
+    if (threadIdx.x >= 64) return;
+    const int lane = threadIdx.x, np = R * TOPK;
+    if (lane < 8) rt.mask[lane] = 0u;
+    #pragma unroll
+    for (int i = 0; i < MAXSLOT * MAXR / 256; ++i)
+        *(f32x4*) &(&rt.w[0][0])[(i * 64 + lane) * 4] = (f32x4) {0.f, 0.f, 0.f, 0.f};
+    wave_lds_sync();
+    int e[2];
+    float wv[2];
+    #pragma unroll
+    for (int h = 0; h < 2; ++h)
+    {
+        const int p = lane + 64 * h;
+        e[h] = -1; wv[h] = 0.f;
+        if (p < np)
+        {
+            const int64_t s = sel[p] - lo;
+            if (s >= 0 && s < n_hot) { e[h] = (int) s; wv[h] = (float) __builtin_bit_cast(_Float16, rw[p]); }
+        }
+        if (e[h] >= 0) atomicOr(&rt.mask[e[h] >> 5], 1u << (e[h] & 31));
+    }
+    wave_lds_sync();
+    unsigned mk[8];
+    #pragma unroll
+    for (int wd = 0; wd < 8; ++wd) mk[wd] = rt.mask[wd];
+    #pragma unroll
+    for (int h = 0; h < 2; ++h)
+        if (e[h] >= 0)
+        {
+            int slot = __popc(mk[e[h] >> 5] & ((1u << (e[h] & 31)) - 1u));
+            #pragma unroll
+            for (int wd = 0; wd < 8; ++wd) slot += wd < (e[h] >> 5) ? __popc(mk[wd]) : 0;
+            rt.e[slot] = (short) e[h];
+            rt.w[slot][(lane + 64 * h) / TOPK] = wv[h];
+        }
+    if (lane == 0) { int m = 0; for (int wd = 0; wd < 8; ++wd) m += __popc(mk[wd]); rt.m = m; }
+    wave_lds_sync();
 }
 
 // route() from sel / rw in LDS or global memory (generic loads)
@@ -169,13 +223,9 @@ __global__ void __launch_bounds__(GW * 64) gu7_kernel(
     const int b = blockIdx.x, G = gridDim.x;
     const bool live = tok < R;
     // Loads are issued in the order they are consumed (the wait counter is in order) and unconditionally (a load
-    // under a branch makes the compiler wait for every outstanding load where the paths meet): x, the window's
-    // pointer tables (x standing in without a window), the given picks, the logits of the wave's rows, then the
-    // shared units.
-    const uint16_t* xr = (const uint16_t*) x + (size_t) (live ? tok : 0) * H + 512 * w + 8 * ks;
-    u32x4 raw[16];
-    #pragma unroll
-    for (int t = 0; t < 16; ++t) raw[t] = ld16(xr + 32 * t);
+    // under a branch makes the compiler wait for every outstanding load where the paths meet): the window's pointer
+    // tables (x standing in without a window), the given picks, the logits of the wave's rows and the bias, the first
+    // half of x, then both shared units; the second half of x follows the routing prologue.
     const int te = min((int) threadIdx.x, max(n_hot - 1, 0));
     const bool hot = n_hot > 0;
     const int64_t* xt = (const int64_t*) x;
@@ -192,8 +242,16 @@ __global__ void __launch_bounds__(GW * 64) gu7_kernel(
         load_bias_global(bias, logits, E, r0.b);
     }
     __builtin_amdgcn_sched_barrier(0);
-    // the first shared unit goes out before the routing prologue (the second right after it: both at once would
-    // not fit the registers next to x)
+    // the rows' x for this wave's k range: k step t covers k = 512 w + 32 t + 8 ks .. + 8 of row tok (A operand), read
+    // as buffer loads in two halves of 8 k steps: a lane of a row past R reads out of range (no memory traffic; its MFMA
+    // row is never stored). The first half (the first shared unit's k steps) goes out now, the second after the
+    // routing prologue, so that both shared units' tiles fit the registers while the prologue runs.
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void*) x, (short) 0, R * H * 2, 0x00020000);
+    const int xoff = live ? (tok * H + 512 * w + 8 * ks) * 2 : 0x40000000;
+    u32x4 raw[16];
+    #pragma unroll
+    for (int t = 0; t < 8; ++t) raw[t] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff + 64 * t, 0, 0);
+    // both shared units (k steps 16 w .. + 8 and + 8 .. + 16) go out before the routing prologue, so their loads cover it
     GuItem A, B;
     const uint8_t* shm = (b & 1) ? sh_uw : sh_gw;
     const uint8_t* shbase = shm + ((size_t) ((b >> 1) * KS_H + 16 * w) * 64 + l) * 16;
@@ -204,53 +262,87 @@ __global__ void __launch_bounds__(GW * 64) gu7_kernel(
         {
             A.g[q] = ldw16(shbase + q * 1024); A.u[q] = ldw16(shbase + (4 + q) * 1024);
         }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    // the rows' x for this wave's k range: k step t covers k = 512 w + 32 t + 8 ks .. + 8 of row tok (A operand)
-    f16x8 xa[16];
-    {
-        const uint32_t lm = live ? 0xffffffffu : 0u;
         #pragma unroll
-        for (int t = 0; t < 16; ++t)
+        for (int q = 0; q < 4; ++q)
         {
-            const u32x4 v = raw[t] & lm;
-            xa[t] = xf ? as_f16x8(v) : bf8_to_f16(v);
+            B.g[q] = ldw16(shbase + (8 + q) * 1024); B.u[q] = ldw16(shbase + (12 + q) * 1024);
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    f16x8 xa[16];
+    #pragma unroll
+    for (int t = 0; t < 8; ++t) xa[t] = xf ? as_f16x8(raw[t]) : bf8_to_f16(raw[t]);
     // every thread stores (threads past n_hot repeat entry n_hot - 1 with its own value)
     tab[0][te] = (const uint8_t*) t0; tab[1][te] = (const uint8_t*) t1;
     tab[2][te] = (const uint8_t*) t2; tab[3][te] = (const uint8_t*) t3;
     if (logits)
     {
+        bias_or_zero(r0.b, bias != nullptr);
         if (w < R) select_from(r0, E, topk, scale, ssel + w * TOPK, srw + w * TOPK);
         #pragma unroll
         for (int i = 0; i < 4; ++i) r1.b[i] = r0.b[i];
         if (w + GW < R) select_from(r1, E, topk, scale, ssel + (w + GW) * TOPK, srw + (w + GW) * TOPK);
         __syncthreads();
-        if (b == 0 && threadIdx.x < R * TOPK) { sel[threadIdx.x] = ssel[threadIdx.x]; rw[threadIdx.x] = srw[threadIdx.x]; }
-        route(ssel, srw, R, lo, n_hot, rt);
+        // wave 0: the selection out (workgroup 0), the distinct experts, then their pointers and the routing record
+        if (w == 0)
+        {
+            if (b == 0)
+            {
+                #pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    if (l + 64 * h < R * TOPK) { sel[l + 64 * h] = ssel[l + 64 * h]; rw[l + 64 * h] = srw[l + 64 * h]; }
+            }
+            route_wave(ssel, srw, R, lo, n_hot, rt);
+            const int m = rt.m;
+            #pragma unroll
+            for (int h = 0; h < 2; ++h)
+            {
+                const int j = l + 64 * h;
+                if (j < m)
+                {
+                    const int e = rt.e[j];
+                    ptr[0][j] = tab[0][e]; ptr[1][j] = tab[1][e]; ptr[2][j] = tab[2][e]; ptr[3][j] = tab[3][e];
+                }
+            }
+            if (b == 0)
+            {
+                int* rec = (int*) (act + (size_t) REC_SLOT * MAXR * I);
+                if (l == 0) rec[0] = m;
+                #pragma unroll
+                for (int h = 0; h < 2; ++h) if (l + 64 * h < m) rec[REC_E + l + 64 * h] = rt.e[l + 64 * h];
+            }
+            if (m == 0 && l < 4) ptr[l][0] = shm;
+        }
     }
-    else route_picks(pk, R, lo, n_hot, rt);
-    const int m = rt.m;
-    if (threadIdx.x < m)
+    else
     {
-        const int e = rt.e[threadIdx.x];
-        ptr[0][threadIdx.x] = tab[0][e]; ptr[1][threadIdx.x] = tab[1][e];
-        ptr[2][threadIdx.x] = tab[2][e]; ptr[3][threadIdx.x] = tab[3][e];
+        route_picks(pk, R, lo, n_hot, rt);
+        const int m = rt.m;
+        if (threadIdx.x < m)
+        {
+            const int e = rt.e[threadIdx.x];
+            ptr[0][threadIdx.x] = tab[0][e]; ptr[1][threadIdx.x] = tab[1][e];
+            ptr[2][threadIdx.x] = tab[2][e]; ptr[3][threadIdx.x] = tab[3][e];
+        }
+        // the routing record for the down launch: m and the local expert id of every slot
+        if (b == 0)
+        {
+            int* rec = (int*) (act + (size_t) REC_SLOT * MAXR * I);
+            if (threadIdx.x == 0) rec[0] = m;
+            if (threadIdx.x < m) rec[REC_E + threadIdx.x] = rt.e[threadIdx.x];
+        }
+        if (m == 0 && threadIdx.x < 4) ptr[threadIdx.x][0] = shm;
     }
-    // the routing record for the down launch: m and the local expert id of every slot
-    if (b == 0)
-    {
-        int* rec = (int*) (act + (size_t) REC_SLOT * MAXR * I);
-        if (threadIdx.x == 0) rec[0] = m;
-        if (threadIdx.x < m) rec[REC_E + threadIdx.x] = rt.e[threadIdx.x];
-    }
-    // no routed expert: slot 0 stands in as the shared matrix (25 MB, beyond every offset a stand-in load reaches)
-    if (m == 0 && threadIdx.x < 4) ptr[threadIdx.x][0] = shm;
+    // (no routed expert: slot 0 stands in as the shared matrix, 25 MB, beyond every offset a stand-in load reaches)
     __syncthreads();
+    const int m = rt.m;
     const int total = m * NB_I;
     const int nr = b < total ? (total - 1 - b) / G + 1 : 0;
     if (!SH && nr == 0) return;                                // uniform over the workgroup
+    // the second half of x (k steps 8 .. 16), ahead of the routed loads, so that waiting for it waits for none of them
+    #pragma unroll
+    for (int t = 8; t < 16; ++t) raw[t] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff + 64 * t, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
     const DqConsts dq = dq_consts();
     // routed item i < nr; past the end (the ring's last prefetch, or no routed item at all) the four loads of a
     // matrix all read one tile (k stride 0): 1 KB instead of repeating the item's 4 KB (an integer select: a pointer
@@ -294,18 +386,18 @@ __global__ void __launch_bounds__(GW * 64) gu7_kernel(
     };
     if (SH)
     {
-        // the shared units (A: k steps 16 w .. + 8, B: + 8 .. + 16) interleaved with the first routed prefetches
-        #pragma unroll
-        for (int q = 0; q < 4; ++q)
-        {
-            B.g[q] = ldw16(shbase + (8 + q) * 1024); B.u[q] = ldw16(shbase + (12 + q) * 1024);
-        }
+        // the shared units: A against x's first half, then routed item 0's loads into A's registers, then B against
+        // the second half
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         #pragma unroll
         for (int q = 0; q < 4; ++q) acc = mfma16(xa[q], as_f16x8(A.g[q]), acc);
         #pragma unroll
         for (int q = 0; q < 4; ++q) acc = mfma16(xa[4 + q], as_f16x8(A.u[q]), acc);
+        __builtin_amdgcn_sched_barrier(0);
         load(A, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        #pragma unroll
+        for (int t = 8; t < 16; ++t) xa[t] = xf ? as_f16x8(raw[t]) : bf8_to_f16(raw[t]);
         #pragma unroll
         for (int q = 0; q < 4; ++q) acc = mfma16(xa[8 + q], as_f16x8(B.g[q]), acc);
         #pragma unroll
@@ -327,7 +419,13 @@ __global__ void __launch_bounds__(GW * 64) gu7_kernel(
             }
         }
     }
-    else load(A, 0);
+    else
+    {
+        load(A, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        #pragma unroll
+        for (int t = 8; t < 16; ++t) xa[t] = xf ? as_f16x8(raw[t]) : bf8_to_f16(raw[t]);
+    }
     // A holds routed item 0 (or a stand-in)
     for (int i = 0; i < nr; i += 2)
     {
@@ -504,7 +602,9 @@ __global__ void __launch_bounds__(DW * 64) dn6_kernel(
         // kept in a register across the loop (the loop has none to spare)
         int tid;
         asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int) threadIdx.x));
-        const int tl = tid & 15, act_lane = ((tl < R ? tl : 0) * I + 512 * ((tid >> 6) & 3) + 8 * ((tid >> 4) & 3)) * 2;
+        // (a row past R reads out of range: no memory traffic, and its MFMA row is never stored)
+        const int tl = tid & 15, act_lane = tl < R ? (tl * I + 512 * ((tid >> 6) & 3) + 8 * ((tid >> 4) & 3)) * 2
+                                                   : 0x10000000;
         #pragma unroll
         for (int t = 0; t < 16; ++t)
             xa[t] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(act_rs, act_lane + 64 * t,

@@ -125,7 +125,9 @@ __device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcp
 struct RowIn { float lg[4], b[4]; };
 
 // from global memory, every load unconditional (index clamped to E - 1, the logits standing in for a NULL bias), so
-// a kernel can issue them ahead of other loads and select later: the logits of a row, and the bias
+// a kernel can issue them ahead of other loads and select later: the logits of a row, and the bias (raw: a select on
+// the loaded value here would wait for it, and for every load issued before it, where it stands; bias_or_zero()
+// applies the NULL bias where the selection needs the values anyway)
 __device__ __forceinline__ void load_logits_global(const float* __restrict__ lg, int E, float (&out)[4])
 {
     const int lane = threadIdx.x & 63;
@@ -140,84 +142,89 @@ __device__ __forceinline__ void load_bias_global(const float* __restrict__ bias,
     for (int i = 0; i < 4; ++i)
     {
         const int e = min(lane + 64 * i, E - 1);
-        const float bv = ldg<float>(bias ? bias + e : lg + e);
-        out[i] = bias ? bv : 0.0f;
+        out[i] = ldg<float>(bias ? bias + e : lg + e);
     }
+}
+__device__ __forceinline__ void bias_or_zero(float (&b)[4], bool has_bias)
+{
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) b[i] = has_bias ? b[i] : 0.0f;
+}
+
+// the wave's maximum (MAX) or minimum of a 32-bit value, returned from lane 63: quad, 8-lane and 16-lane butterflies,
+// then the row broadcasts into rows 1, 3 and 2, 3 (gfx9 DPP: each step is one max / min whose first operand is read
+// across lanes; a lane of a masked row keeps its value). Two wait states before each DPP read of a VGPR the previous
+// VALU instruction wrote (the s_nop 1).
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_ext_u32(uint32_t v)
+{
+#define HMOE_DPP_STEPS(OP)                                                                                            \
+    "s_nop 1\n\t" OP " %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"                                 \
+    "s_nop 1\n\t" OP " %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"                                 \
+    "s_nop 1\n\t" OP " %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"                                     \
+    "s_nop 1\n\t" OP " %0, %0, %0 row_mirror row_mask:0xf bank_mask:0xf\n\t"                                          \
+    "s_nop 1\n\t" OP " %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"                                        \
+    "s_nop 1\n\t" OP " %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"                                        \
+    "s_nop 1"
+    if (MAX) asm volatile(HMOE_DPP_STEPS("v_max_u32_dpp") : "+v"(v));
+    else asm volatile(HMOE_DPP_STEPS("v_min_u32_dpp") : "+v"(v));
+#undef HMOE_DPP_STEPS
+    return (uint32_t) __builtin_amdgcn_readlane((int) v, 63);
 }
 
 // top-k of one row by a wave (all 64 lanes active): keys of experts lane + 64 i; the selection is the one of taking
 // the largest (key, -index) pair topk times, so ties go to the lowest index and sel is in descending key order
-// (exl3_router.py:106-121); the sum runs over the selected unbiased activations in that order. It is found without
-// those rounds: the topk-th largest key by a bitwise threshold search on wave ballots, then each pick's position from
-// ballot counts; every step is wave-uniform.
+// (exl3_router.py:106-121); the sum runs over the selected unbiased activations in that order. Done as exactly that:
+// each lane sorts its 4 (key, id) pairs (key descending, then id ascending), and each of topk rounds takes the wave's
+// largest lane head (a DPP reduction; on an exact tie of keys the lowest id among the tied heads, by a second one)
+// and pops it from its lane.
 __device__ inline void select_from(const RowIn& in, int E, int topk, float scale, int64_t* __restrict__ sel,
                                    uint16_t* __restrict__ rw)
 {
     const int lane = threadIdx.x & 63;
-    float a[4]; uint32_t key[4];
+    uint32_t k[4], id[4];
+    float a[4];
     #pragma unroll
     for (int i = 0; i < 4; ++i)
     {
         const int e = lane + 64 * i;
-        if (e < E)
-        {
-            a[i] = hmoe_sigmoid(in.lg[i]);
-            key[i] = hmoe_okey(a[i] + in.b[i]);
-        }
-        else { a[i] = 0.f; key[i] = 0u; }
+        const bool ok = e < E;
+        a[i] = ok ? hmoe_sigmoid(in.lg[i]) : 0.f;
+        k[i] = ok ? hmoe_okey(a[i] + in.b[i]) : 0u;          // (a finite float's key is never 0)
+        id[i] = (uint32_t) e;
     }
-    // T: the topk-th largest key (the largest T with at least topk keys >= T), found one bit at a time with wave
-    // ballots (a chain of 32 short steps, where taking the maximum topk times is a chain of cross-lane reductions)
-    uint32_t T = 0u;
-    for (int bit = 31; bit >= 0; --bit)
-    {
-        const uint32_t c = T | (1u << bit);
-        int n = 0;
-        #pragma unroll
-        for (int i = 0; i < 4; ++i) n += __popcll(__ballot(key[i] >= c));
-        if (n >= topk) T = c;
-    }
-    // the picks: every key above T, then keys equal to T by ascending expert id (id lane + 64 i: i-major order)
-    uint64_t pick[4];
-    int need = topk;
-    #pragma unroll
-    for (int i = 0; i < 4; ++i) { pick[i] = __ballot(key[i] > T); need -= __popcll(pick[i]); }
-    #pragma unroll
-    for (int i = 0; i < 4; ++i)
-    {
-        uint64_t eq = __ballot(key[i] == T);
-        while (need > 0 && eq) { const uint64_t low = eq & (~eq + 1ull); pick[i] |= low; eq ^= low; --need; }
-    }
-    // each pick's place in the selection order (key descending, then id ascending): the number of picks before it;
-    // lane r of es / as receives the r-th pick's id and sigmoid
+    // the lane's 4 pairs in selection order (a 5-comparator network; ids start ascending)
+    auto cas = [&](int p, int q) {
+        const bool sw = k[q] > k[p] || (k[q] == k[p] && id[q] < id[p]);
+        const uint32_t tk = k[p], ti = id[p];
+        const float ta = a[p];
+        k[p] = sw ? k[q] : k[p]; id[p] = sw ? id[q] : id[p]; a[p] = sw ? a[q] : a[p];
+        k[q] = sw ? tk : k[q]; id[q] = sw ? ti : id[q]; a[q] = sw ? ta : a[q];
+    };
+    cas(0, 1); cas(2, 3); cas(0, 2); cas(1, 3); cas(1, 2);
+    // topk rounds; lane r of es / as receives the r-th pick's id and activation
     int es = 0;
     float as = 0.f;
-    #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int r = 0; r < topk; ++r)
     {
-        uint64_t mk = pick[i];
-        while (mk)
-        {
-            const int l = __builtin_ctzll(mk);
-            mk &= mk - 1ull;
-            const uint32_t kx = (uint32_t) __builtin_amdgcn_readlane((int) key[i], l);
-            const int ex = l + 64 * i;
-            int r = 0;
-            #pragma unroll
-            for (int j = 0; j < 4; ++j)
-            {
-                const int ej = lane + 64 * j;
-                const bool before = ((pick[j] >> lane) & 1ull) && (key[j] > kx || (key[j] == kx && ej < ex));
-                r += __popcll(__ballot(before));
-            }
-            const int ax = __builtin_amdgcn_readlane(__float_as_int(i == 0 ? a[0] : i == 1 ? a[1] : i == 2 ? a[2] : a[3]), l);
-            es = lane == r ? ex : es;
-            as = lane == r ? __int_as_float(ax) : as;
-        }
+        const uint32_t mk = wave_ext_u32<true>(k[0]);
+        const uint64_t tie = __ballot(k[0] == mk);
+        int wl = __builtin_ctzll(tie);                          // the lane of the winning head
+        if (__popcll(tie) > 1)                                  // equal keys: the lowest id among the tied heads
+            wl = (int) (wave_ext_u32<false>(k[0] == mk ? id[0] : 0xffffffffu) & 63u);
+        const int ex = __builtin_amdgcn_readlane((int) id[0], wl);
+        const float aw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[0]), wl));
+        es = lane == r ? ex : es;
+        as = lane == r ? aw : as;
+        const bool win = lane == wl;
+        k[0] = win ? k[1] : k[0]; id[0] = win ? id[1] : id[0]; a[0] = win ? a[1] : a[0];
+        k[1] = win ? k[2] : k[1]; id[1] = win ? id[2] : id[1]; a[1] = win ? a[2] : a[1];
+        k[2] = win ? k[3] : k[2]; id[2] = win ? id[3] : id[2]; a[2] = win ? a[3] : a[2];
+        k[3] = win ? 0u : k[3];
     }
     // the unbiased sigmoids summed in selection order, from 0
     float sum = 0.f;
-    for (int k = 0; k < topk; ++k) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(as), k));
+    for (int kk = 0; kk < topk; ++kk) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(as), kk));
     if (lane < topk)
     {
         sel[lane] = es;
