@@ -211,7 +211,7 @@ __global__ void __launch_bounds__(GW * 64) gu7_kernel(
     int topk, float scale, int64_t* __restrict__ sel, uint16_t* __restrict__ rw, int R, int lo, int n_hot,
     const int64_t* __restrict__ gate_w, const int64_t* __restrict__ up_w, const int64_t* __restrict__ gate_s,
     const int64_t* __restrict__ up_s, const uint8_t* __restrict__ sh_gw, const uint8_t* __restrict__ sh_uw,
-    _Float16* __restrict__ act)
+    _Float16* __restrict__ act, int G)
 {
     __shared__ Route rt;
     __shared__ const uint8_t* tab[4][HMOE_MAXE];
@@ -220,8 +220,11 @@ __global__ void __launch_bounds__(GW * 64) gu7_kernel(
     __shared__ uint16_t srw[MAXR * TOPK];
     __shared__ f32x4 red[2][GW][2][64];
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63, tok = l & 15, ks = l >> 4, row = l & 15;
-    const int b = blockIdx.x, G = gridDim.x;
+    const int b = blockIdx.x;                                 // (G: the grid, passed: gridDim reads the dispatch packet)
     const bool live = tok < R;
+    // the arguments in the kernel-argument segment's last cache line, read with the first ones: read where first used
+    // (the compiler's choice), that scalar load's wait would come at the first workgroup barrier, under the stream
+    asm volatile("" :: "s"(act), "s"(G));
     // Loads are issued in the order they are consumed (the wait counter is in order) and unconditionally (a load
     // under a branch makes the compiler wait for every outstanding load where the paths meet): the window's pointer
     // tables (x standing in without a window), the given picks, the logits of the wave's rows and the bias, the first
@@ -309,7 +312,11 @@ __global__ void __launch_bounds__(GW * 64) gu7_kernel(
                 int* rec = (int*) (act + (size_t) REC_SLOT * MAXR * I);
                 if (l == 0) rec[0] = m;
                 #pragma unroll
-                for (int h = 0; h < 2; ++h) if (l + 64 * h < m) rec[REC_E + l + 64 * h] = rt.e[l + 64 * h];
+                for (int h = 0; h < 2; ++h)
+                {
+                    const int j = l + 64 * h;
+                    rec[REC_E + j] = (j < m ? rt.e[j] : 0) | (m << 16);
+                }
             }
             if (m == 0 && l < 4) ptr[l][0] = shm;
         }
@@ -329,7 +336,7 @@ __global__ void __launch_bounds__(GW * 64) gu7_kernel(
         {
             int* rec = (int*) (act + (size_t) REC_SLOT * MAXR * I);
             if (threadIdx.x == 0) rec[0] = m;
-            if (threadIdx.x < m) rec[REC_E + threadIdx.x] = rt.e[threadIdx.x];
+            if (threadIdx.x < MAXSLOT) rec[REC_E + threadIdx.x] = ((int) threadIdx.x < m ? rt.e[threadIdx.x] : 0) | (m << 16);
         }
         if (m == 0 && threadIdx.x < 4) ptr[threadIdx.x][0] = shm;
     }
@@ -461,7 +468,7 @@ template <bool SH, int NJ>
 __global__ void __launch_bounds__(DW * 64) dn6_kernel(
     int R, int n_hot, const int64_t* __restrict__ down_w, const int64_t* __restrict__ down_s,
     const _Float16* __restrict__ act, const uint8_t* __restrict__ sh_dw, float* __restrict__ y32,
-    int* __restrict__ nparts_out)
+    int* __restrict__ nparts_out, int G)
 {
     // one LDS block laid out by hand: the reduction buffer and the tables at the bottom, so that every access in the
     // item loop is one base register plus an immediate offset (below 64 KB), then the shared act
@@ -474,7 +481,8 @@ __global__ void __launch_bounds__(DW * 64) dn6_kernel(
     auto& red = *reinterpret_cast<f32x4 (*)[2][DW][64]>(smem + O_RED);
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
     const int sw = w >> 2, kq = w & 3;                          // routed items: slot of the quad, k quarter of I
-    const int G = gridDim.x, b = blockIdx.x;
+    const int b = blockIdx.x;                                 // (G: the grid, passed: gridDim reads the dispatch packet)
+    asm volatile("" :: "s"(sh_dw), "s"(G));                   // (read with the first arguments, as in gu7_kernel)
     const int part0 = SH ? 1 : 0, nsh = SH ? NB_H : 0;
     const int s_mine = SH ? (b + G < NB_H ? 2 : 1) : 0;       // (G <= NB_H: every workgroup has one)
     // loads in issue order: pointer tables, the gate/up launch's routing record (slot count and the local expert of
@@ -485,7 +493,9 @@ __global__ void __launch_bounds__(DW * 64) dn6_kernel(
     const int* rec = (const int*) (act + (size_t) REC_SLOT * MAXR * I);
     const int64_t t0 = ldg<int64_t>(n_hot > 0 ? down_w + te : (const int64_t*) rec);
     const int64_t t1 = ldg<int64_t>(n_hot > 0 ? down_s + te : (const int64_t*) rec);
-    const int rm = ldg<int>(rec), re = ldg<int>(rec + REC_E + min((int) threadIdx.x, MAXSLOT - 1));
+    // (the slot count comes with every slot's entry, read by lane loads: word 0 read from its uniform address would be a
+    // scalar load, whose wait, on the scalar counter, comes before the shared tiles' loads and holds them back)
+    const int re = ldg<int>(rec + REC_E + min((int) threadIdx.x, MAXSLOT - 1));
     __builtin_amdgcn_sched_barrier(0);                          // keep the routing loads ahead of the item loads
     // shared items: wave w owns k group w of I (4 k steps of F16T) with the shared act of its k group as the A operand.
     // The act f16(silu(g) u) of the R live rows is formed once per workgroup into xsh, 4 elements per thread in each
@@ -528,10 +538,10 @@ __global__ void __launch_bounds__(DW * 64) dn6_kernel(
     // would pull the table loads into it, behind the item loads
     tab[0][te] = (const uint8_t*) t0; tab[1][te] = (const uint8_t*) t1;
     __syncthreads();
-    const int m = min(max(rm, 0), min(n_hot, MAXSLOT)), nq = (m + 3) / 4;
+    const int m = min(max(__builtin_amdgcn_readfirstlane(re) >> 16, 0), min(n_hot, MAXSLOT)), nq = (m + 3) / 4;
     if (threadIdx.x < m)
     {
-        const int e = min(max(re, 0), n_hot - 1);
+        const int e = min(re & 0xffff, n_hot - 1);
         ptr[0][threadIdx.x] = tab[0][e]; ptr[1][threadIdx.x] = tab[1][e];
     }
     // no routed expert: slot 0 stands in as act, so the first routed load below stays unconditional and in bounds
@@ -754,11 +764,12 @@ static int run_decode(const DecodeArgs& a, int phases, hipStream_t st)
         if (sh)
             gu7_kernel<true><<<GU_SH_GRID, GW * 64, 0, st>>>(a.x, a.xf, a.logits, a.bias, a.E, a.topk, a.scale, so, ro, R,
                                                              a.lo, a.n_hot, a.gate_w, a.up_w, a.gate_s, a.up_s,
-                                                             (const uint8_t*) a.sh_gw, (const uint8_t*) a.sh_uw, a.act);
+                                                             (const uint8_t*) a.sh_gw, (const uint8_t*) a.sh_uw, a.act,
+                                                             GU_SH_GRID);
         else
             gu7_kernel<false><<<G, GW * 64, 0, st>>>(a.x, a.xf, a.logits, a.bias, a.E, a.topk, a.scale, so, ro, R,
                                                      a.lo, a.n_hot, a.gate_w, a.up_w, a.gate_s, a.up_s, nullptr,
-                                                     nullptr, a.act);
+                                                     nullptr, a.act, G);
     }
     if (phases & 4)
     {
@@ -768,10 +779,11 @@ static int run_decode(const DecodeArgs& a, int phases, hipStream_t st)
             // NJ: float4 steps per thread to form the shared act of R rows (R * 512 float4 over 1024 threads)
             auto k = R <= 2 ? dn6_kernel<true, 1> : R <= 4 ? dn6_kernel<true, 2> : R <= 8 ? dn6_kernel<true, 4>
                                                                                         : dn6_kernel<true, 8>;
-            k<<<gd, DW * 64, 0, st>>>(R, a.n_hot, a.down_w, a.down_s, a.act, (const uint8_t*) a.sh_dw, a.y32, a.ctr);
+            k<<<gd, DW * 64, 0, st>>>(R, a.n_hot, a.down_w, a.down_s, a.act, (const uint8_t*) a.sh_dw, a.y32, a.ctr, gd);
         }
         else
-            dn6_kernel<false, 1><<<gd, DW * 64, 0, st>>>(R, a.n_hot, a.down_w, a.down_s, a.act, nullptr, a.y32, a.ctr);
+            dn6_kernel<false, 1><<<gd, DW * 64, 0, st>>>(R, a.n_hot, a.down_w, a.down_s, a.act, nullptr, a.y32, a.ctr,
+                                                         gd);
     }
     if (phases & 8) dec_d_kernel<<<(R * H + 255) / 256, 256, 0, st>>>(a.y32, a.ctr, R, a.y, a.out);
     return HMOE_LAUNCHED("moe4");

@@ -21,7 +21,8 @@ constexpr int SH_SLOT = MAXSLOT;            // act slot of the shared expert
 constexpr int SHP_SLOT = MAXSLOT + 1;       // the shared expert's fp32 gate and up sums [2][MAXR][I] (4 slots' room)
 constexpr int REC_SLOT = SHP_SLOT + 4;      // the gate/up launch's routing record for the down launch (int words)
 constexpr int ACT_SLOTS = REC_SLOT + 1;
-constexpr int REC_E = 64;                   // record: word 0 = distinct experts m, words REC_E + j = local id of slot j
+constexpr int REC_E = 64;                   // record: word 0 = distinct experts m, words REC_E + j (j < MAXSLOT) = local
+                                            // id of slot j (0 past m) | m << 16, so every lane's word carries m
 
 // I4G128 group scales: 128-byte blocks of 16 rows x 4 k groups; the index (in bf16 units) of row n's scale of group g
 // (KG = K / 128 groups, a multiple of 4)
@@ -411,7 +412,7 @@ __device__ inline void pair_logits(const uint16_t* __restrict__ x, const NormIn&
                 v[e] = (uint32_t) hmoe_f2bf((a0 * rf) * b0) | ((uint32_t) hmoe_f2bf((a1 * rf) * b1) << 16);
             }
             *(u32x4*) &xs[j][(q >> 2) * XST + 4 * (q & 3)] = v;
-            if (r0 + j < R && (int) ((q * gridDim.x) / 768) == (int) blockIdx.x)
+            if (r0 + j < R && (int) ((q * ((E + EPW - 1) / EPW)) / 768) == (int) blockIdx.x)
             {
                 *(u32x4*) (nin.xn + (size_t) row * H + 8 * q) = v;
                 if (nin.xh)

@@ -137,9 +137,11 @@ struct Block { int e, p0, rows; };
 // XCDs (workgroup i runs on XCD i % 8), each with its own L2: the column blocks of one row block go to consecutive
 // workgroups of one XCD, so they run together and read the block's input rows from that XCD's L2 (one fetch from
 // memory instead of one per column block). The grid's x extent is a multiple of 8 (pgemm_grid).
-__device__ __forceinline__ void xcd_tile(int& rb, int& cb)
+// (the grid's extents come from the launch's own arguments: gridDim reads the dispatch packet, a round trip to the
+// queue's memory at every workgroup start)
+__device__ __forceinline__ void xcd_tile(int& rb, int& cb, int gx, int ny)
 {
-    const int i = blockIdx.x + gridDim.x * blockIdx.y, j = i >> 3, ny = gridDim.y;
+    const int i = blockIdx.x + gx * blockIdx.y, j = i >> 3;
     rb = (j / ny) * 8 + (i & 7);
     cb = j % ny;
 }
@@ -202,7 +204,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
     __shared__ __attribute__((aligned(16))) u32x4 xs0[NTT * 4 * 64];
     __shared__ __attribute__((aligned(16))) u32x4 xs1[NTT * 4 * 64];
     int rbi, cbi;
-    xcd_tile(rbi, cbi);
+    xcd_tile(rbi, cbi, (nrb + 7) & ~7, NOUT / (16 * NS * NWV));
     Block rb;
     if (!get_block(rbt, nrb, meta, n_tab, np, rbi, rb)) return;
     // a block of more than PBX picks runs as passes of PBX, one after the other (a later pass reads the weights
@@ -434,10 +436,11 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
     }
 }
 
-// x bf16 -> f16 (the GEMM input when the caller has no f16 copy)
+// x bf16 -> f16 (the GEMM input when the caller has no f16 copy), on a grid of TF16_GRID workgroups
+constexpr int TF16_GRID = 1024;
 __global__ void __launch_bounds__(256) to_f16_kernel(const uint16_t* __restrict__ x, size_t n, _Float16* __restrict__ xh)
 {
-    for (size_t i = (blockIdx.x * (size_t) 256 + threadIdx.x) * 8; i < n; i += (size_t) gridDim.x * 256 * 8)
+    for (size_t i = (blockIdx.x * (size_t) 256 + threadIdx.x) * 8; i < n; i += (size_t) TF16_GRID * 256 * 8)
     {
         const u32x4 v = ld16(x + i);
         f16x8 o;
@@ -564,7 +567,7 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
     if (xf == HMOE_XF_BF16)
     {
         HMOE_REQUIRE(gu && ((uintptr_t) gu & 15) == 0, "moe4p_forward: xf = 0 needs the gu scratch (the f16 copy of x)");
-        to_f16_kernel<<<1024, 256, 0, st>>>(xb, (size_t) T * H, (_Float16*) gu);
+        to_f16_kernel<<<TF16_GRID, 256, 0, st>>>(xb, (size_t) T * H, (_Float16*) gu);
         xb = (const uint16_t*) gu;
     }
     _Float16* a = (_Float16*) ar;
@@ -623,7 +626,7 @@ extern "C" int hmoe_shared_forward(const void* x, int T, const void* sh_gw, cons
     const _Float16* xs = (const _Float16*) x;
     if (xf == HMOE_XF_BF16)
     {
-        to_f16_kernel<<<1024, 256, 0, st>>>((const uint16_t*) x, (size_t) T * H, (_Float16*) wk);
+        to_f16_kernel<<<TF16_GRID, 256, 0, st>>>((const uint16_t*) x, (size_t) T * H, (_Float16*) wk);
         xs = (const _Float16*) wk;
     }
     _Float16* a = (_Float16*) (wk + shw_act(T));
@@ -673,7 +676,7 @@ extern "C" int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid,
         // the f16 copy of x in d (the reference gathers the picks' rows into d; T rows fit: T * H * 2 <= npos * H * 4
         // whenever every token has a pick, and the check below holds it in general)
         HMOE_REQUIRE(d && (size_t) T * H * 2 <= (size_t) ps * H * 4, "moe4t_forward: bf16 x needs d for its f16 copy");
-        to_f16_kernel<<<1024, 256, 0, st>>>((const uint16_t*) x, (size_t) T * H, (_Float16*) d);
+        to_f16_kernel<<<TF16_GRID, 256, 0, st>>>((const uint16_t*) x, (size_t) T * H, (_Float16*) d);
         xh = (const _Float16*) d;
     }
     if (nrb > 0)

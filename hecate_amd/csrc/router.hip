@@ -21,7 +21,7 @@ __global__ void __launch_bounds__(512) router_logits_h_kernel(
     pair_logits<false>(x, NormIn{}, wt, 2 * blockIdx.x, E, R, logits);
     if (xh)
     {
-        const int n = R * H, per = (n + gridDim.x - 1) / gridDim.x, b0 = blockIdx.x * per;
+        const int nb = (E + 1) / 2, n = R * H, per = (n + nb - 1) / nb, b0 = blockIdx.x * per;   // (nb: the grid)
         to_f16_range(x, xh, b0, min(n, b0 + per), threadIdx.x, blockDim.x);
     }
 }
@@ -35,7 +35,7 @@ __global__ void __launch_bounds__(512) router_logits_kernel(
     expert_logits(x, wt, 2 * blockIdx.x + half, E, R, K, tid, sums[half], logits);
     if (xh)
     {
-        const int n = R * K, per = (n + gridDim.x - 1) / gridDim.x, b0 = blockIdx.x * per;
+        const int nb = (E + 1) / 2, n = R * K, per = (n + nb - 1) / nb, b0 = blockIdx.x * per;   // (nb: the grid)
         to_f16_range(x, xh, b0, min(n, b0 + per), threadIdx.x, blockDim.x);
     }
 }
