@@ -36,7 +36,10 @@ int set_error(int code, const char* fmt, ...);
 // the prefill shared expert (shared_gemm.hip), f16 row-major operands: act [T][I] = f16(silu(wg x) (wu x)), and
 // out [T][H] = wd act (fp32, written or, with add, added into)
 int dense_gate_up(const _Float16* wg, const _Float16* wu, const _Float16* x, int T, _Float16* act, hipStream_t st);
-int dense_down(const _Float16* wd, const _Float16* act, int T, float* out, bool add, hipStream_t st);
+// the shared expert's down projection over T tokens: out rows [T][H] stored as f16 (DG_MODE_F16) or added into fp32
+// (DG_MODE_ADD)
+enum { DG_MODE_F16 = 0, DG_MODE_ADD = 1 };
+int dense_down(const _Float16* wd, const _Float16* act, int T, void* out, int mode, hipStream_t st);
 int hip_check(hipError_t e, const char* what);
 #define HMOE_REQUIRE(cond, ...) do { if (!(cond)) return ::hmoe::set_error(HMOE_ERR_ARG, __VA_ARGS__); } while (0)
 #define HMOE_LAUNCHED(what) ::hmoe::hip_check(hipGetLastError(), what)

@@ -178,8 +178,9 @@ struct PFetch
 };
 
 // epilogues: gate/up -> act f16 (EPI_ACT) or the raw gate and up sums (EPI_RAW, fp32 [2][ps][I], the test entry of
-// moe4t); down -> d fp32 rows (EPI_D) or added into out[tok] with fp32 atomics (EPI_FIN, moe4t.cu's down epilogue)
-enum { EPI_ACT = 0, EPI_RAW = 1, EPI_D = 2, EPI_FIN = 3 };
+// moe4t); down -> d f16 rows for the ordered combine (EPI_D16), d fp32 rows (EPI_D, the moe4t.gemm test entry) or
+// added into out[tok] with fp32 atomics (EPI_FIN, moe4t.cu's down epilogue)
+enum { EPI_ACT = 0, EPI_RAW = 1, EPI_D = 2, EPI_FIN = 3, EPI_D16 = 4 };
 
 // NTT: 16-pick tiles per pass (8: 128 picks, 4 waves; 16: 256 picks, 8 waves, one pass for the long prefill's 256-pick
 // blocks, each dequantised weight fragment feeding twice the MFMAs); NWV waves, each staging two tiles
@@ -430,6 +431,14 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
                         for (int i = 0; i < 4; ++i) unsafeAtomicAdd(o + i, acc[st][0][tt][i]);
                     }
                 }
+                else if (EPI == EPI_D16)
+                {
+                    // (a pick's down row rounded to f16: half the bytes written here and read by the combine)
+                    _Float16 o[4];
+                    #pragma unroll
+                    for (int i = 0; i < 4; ++i) o[i] = (_Float16) acc[st][0][tt][i];
+                    *(uint2*) ((_Float16*) dout + (size_t) (off + b.p0 + pk) * NOUT + n) = *(const uint2*) o;
+                }
                 else *(f32x4*) (dout + (size_t) (off + b.p0 + pk) * NOUT + n) = acc[st][0][tt];
             }
         }
@@ -454,10 +463,10 @@ __global__ void __launch_bounds__(256) to_f16_kernel(const uint16_t* __restrict_
     }
 }
 
-// fin, deterministic: out[t] += (sum over k in top-k order of d[inv[t][k]]) (+ the shared expert's row). Every row's
-// load is unconditional (an absent pick or shared row reads row 0 and is dropped by a select at its add), so all of
-// them are in flight together: under a branch each load was followed by a wait for it.
-__global__ void __launch_bounds__(256) pfin_kernel(const float* __restrict__ d, const int* __restrict__ inv, int topk,
+// fin, deterministic: out[t] += (sum over k in top-k order of d[inv[t][k]]) (+ the shared expert's row), the d rows f16,
+// summed in fp32. Every row's load is unconditional (an absent pick or shared row reads row 0 and is dropped by a
+// select at its add), so all of them are in flight together: under a branch each load was followed by a wait for it.
+__global__ void __launch_bounds__(256) pfin_kernel(const _Float16* __restrict__ d, const int* __restrict__ inv, int topk,
                                                    int np, int sh_off, float* __restrict__ out)
 {
     constexpr int NR = HMOE_TOPK + 1;
@@ -475,14 +484,20 @@ __global__ void __launch_bounds__(256) pfin_kernel(const float* __restrict__ d, 
     pos[HMOE_TOPK] = sh_off >= 0 ? sh_off + t : 0;
     for (int n = threadIdx.x * 4; n < H; n += 256 * 4)
     {
-        f32x4 v[NR];
+        f16x4 v[NR];
         #pragma unroll
-        for (int k = 0; k < NR; ++k) v[k] = *(const f32x4*) (d + (size_t) pos[k] * H + n);
+        for (int k = 0; k < NR; ++k) v[k] = *(const f16x4*) (d + (size_t) pos[k] * H + n);
         f32x4* o = (f32x4*) (out + (size_t) t * H + n);
         const f32x4 ov = *o;
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
         #pragma unroll
-        for (int k = 0; k < NR; ++k) s = use[k] ? s + v[k] : s;
+        for (int k = 0; k < NR; ++k)
+        {
+            f32x4 vk;
+            #pragma unroll
+            for (int i = 0; i < 4; ++i) vk[i] = (float) v[k][i];
+            s = use[k] ? s + vk : s;
+        }
         *o = ov + s;
     }
 }
@@ -534,7 +549,7 @@ extern "C" size_t hmoe_moe4p_scratch_bytes(int which, int ps, int T)
     {
         case 0: return SH_X_BYTES(T);                                   // gu: the f16 copy of x
         case 1: return (size_t) (ps + T) * I * 2;                       // ar f16 [ps + T][I]
-        case 2: return (size_t) (ps + T) * H * 4;                       // d fp32 [ps + T][H]
+        case 2: return (size_t) (ps + T) * H * 4;                       // d [ps + T][H]: f16 rows (fp32-sized, as the reference)
         default: return 0;
     }
 }
@@ -578,8 +593,8 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
         pgemm_kernel<2, 2, 2><<<pgemm_grid(nrb, I / 128), PT, 0, st>>>((const _Float16*) xb, tok, wt, rbt, nrb, meta,
             n_tab, gw, uw, gs, us, a, nullptr, T, 0, npos);
         if (inv)
-            pgemm_kernel<1, 4, 2><<<pgemm_grid(nrb, H / 256), PT, 0, st>>>(a, nullptr, nullptr, rbt, nrb, meta, n_tab, dw,
-                nullptr, ds, nullptr, nullptr, d, T, 0, npos);
+            pgemm_kernel<1, 4, 2, EPI_D16><<<pgemm_grid(nrb, H / 256), PT, 0, st>>>(a, nullptr, nullptr, rbt, nrb, meta,
+                n_tab, dw, nullptr, ds, nullptr, nullptr, d, T, 0, npos);
         else
             pgemm_kernel<1, 4, 2, EPI_FIN><<<pgemm_grid(nrb, H / 256), PT, 0, st>>>(a, tok, nullptr, rbt, nrb, meta, n_tab,
                 dw, nullptr, ds, nullptr, nullptr, nullptr, T, 0, npos, out);
@@ -587,15 +602,16 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
     const bool sh = sh_gw != nullptr;
     if (sh)
     {
-        // the shared expert on every token: act rows ps.. = f16(silu(gate x) up x), then down into d rows ps.. (fp32),
+        // the shared expert on every token: act rows ps.. = f16(silu(gate x) up x), then down into d rows ps.. (f16),
         // which the ordered combine adds after each token's picks
         if (int rc = dense_gate_up((const _Float16*) sh_gw, (const _Float16*) sh_uw, (const _Float16*) xb, T,
                                    a + (size_t) ps * I, st))
             return rc;
-        if (int rc = dense_down((const _Float16*) sh_dw, a + (size_t) ps * I, T, d + (size_t) ps * H, false, st))
+        if (int rc = dense_down((const _Float16*) sh_dw, a + (size_t) ps * I, T, (_Float16*) d + (size_t) ps * H,
+                                DG_MODE_F16, st))
             return rc;
     }
-    if (inv) pfin_kernel<<<T, 256, 0, st>>>(d, inv, topk, npos, sh ? ps : -1, out);
+    if (inv) pfin_kernel<<<T, 256, 0, st>>>((const _Float16*) d, inv, topk, npos, sh ? ps : -1, out);
     return HMOE_LAUNCHED("moe4p_forward");
 }
 
@@ -632,7 +648,7 @@ extern "C" int hmoe_shared_forward(const void* x, int T, const void* sh_gw, cons
     _Float16* a = (_Float16*) (wk + shw_act(T));
     if (int rc = dense_gate_up((const _Float16*) sh_gw, (const _Float16*) sh_uw, xs, T, a, st)) return rc;
     // (out += each product element once, in the GEMM's epilogue)
-    if (int rc = dense_down((const _Float16*) sh_dw, a, T, out, true, st)) return rc;
+    if (int rc = dense_down((const _Float16*) sh_dw, a, T, out, DG_MODE_ADD, st)) return rc;
     return HMOE_LAUNCHED("shared_forward");
 }
 
@@ -687,13 +703,13 @@ extern "C" int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid,
             gw, uw, gs, us, (_Float16*) ar, nullptr, T, 0, npos);
         // (d held the f16 copy of x, which the gate/up GEMM has consumed by now: the down rows may overwrite it)
         if (inv)
-            pgemm_kernel<1, 2, 4, EPI_D, 16, 8><<<pgemm_grid(nrb, H / 256), 512, 0, st>>>((const _Float16*) ar, nullptr,
-                nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, d, T, 0, npos);
+            pgemm_kernel<1, 2, 4, EPI_D16, 16, 8><<<pgemm_grid(nrb, H / 256), 512, 0, st>>>((const _Float16*) ar,
+                nullptr, nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, d, T, 0, npos);
         else
             pgemm_kernel<1, 2, 4, EPI_FIN, 16, 8><<<pgemm_grid(nrb, H / 256), 512, 0, st>>>((const _Float16*) ar, tok,
                 nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, nullptr, T, 0, npos, out);
     }
-    if (inv) pfin_kernel<<<T, 256, 0, st>>>(d, inv, topk, npos, -1, out);
+    if (inv) pfin_kernel<<<T, 256, 0, st>>>((const _Float16*) d, inv, topk, npos, -1, out);
     return HMOE_LAUNCHED("moe4t_forward");
 }
 

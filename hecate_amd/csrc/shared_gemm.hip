@@ -1,8 +1,8 @@
 // shared_gemm.hip - the prefill shared expert's projections as hand-written dense MFMA GEMMs (f16 operands, fp32
 // accumulation). The shared expert is a dense bf16 MLP (its weights are exact in f16), run over every token of the
 // chunk; the reference keeps it outside its routed op at prefill (runtime/tier/tier_split.py:548-560, the model's own
-// shared-expert forward). gate and up run as one GEMM whose epilogue writes act = f16(silu(g) u); down writes fp32
-// rows (the ordered combine adds them) or adds them into out.
+// shared-expert forward). gate and up run as one GEMM whose epilogue writes act = f16(silu(g) u); down writes f16
+// rows (the ordered combine adds them) or adds them into fp32 out.
 //
 // dgemm_kernel: D[n][m] = sum_k X[n][k] W[m][k] over row-major W [M][K] (one matrix, or gate and up as two) and X
 // [N][K]. Workgroup = WM x WN waves (WM along the weight rows, WN along the tokens) = 16 WM TM / NMAT output rows x
@@ -18,7 +18,7 @@
 
 namespace hmoe {
 
-enum { DG_ACT = 0, DG_D = 1, DG_ADD = 2 };
+enum { DG_ACT = 0, DG_D16 = 1, DG_ADD = 2 };
 
 template <int NMAT, int TM, int TN, int WM, int WN, int EPI>
 __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
@@ -146,10 +146,17 @@ dgemm_kernel(
                 for (int q = 0; q < 4; ++q) o[q] = (_Float16) (silu(acc[i][j][q]) * acc[TMO + i][j][q]);
                 *(uint2*) ((_Float16*) out + (size_t) n * ldo + m) = *(const uint2*) o;
             }
+            else if (EPI == DG_D16)
+            {
+                _Float16 o[4];
+                #pragma unroll
+                for (int q = 0; q < 4; ++q) o[q] = (_Float16) acc[i][j][q];
+                *(uint2*) ((_Float16*) out + (size_t) n * ldo + m) = *(const uint2*) o;
+            }
             else
             {
                 f32x4* o = (f32x4*) ((float*) out + (size_t) n * ldo + m);
-                *o = EPI == DG_ADD ? *o + acc[i][j] : acc[i][j];
+                *o = *o + acc[i][j];
             }
         }
     }
@@ -176,7 +183,7 @@ int hmoe::dense_gate_up(const _Float16* wg, const _Float16* wu, const _Float16* 
     return HMOE_LAUNCHED("shared gate/up");
 }
 
-int hmoe::dense_down(const _Float16* wd, const _Float16* act, int T, float* out, bool add, hipStream_t st)
+int hmoe::dense_down(const _Float16* wd, const _Float16* act, int T, void* out, int mode, hipStream_t st)
 {
     constexpr int BM = 16 * DN_WM * DN_TM, BN = 16 * DN_WN * DN_TN;
     static_assert(H % BM == 0 && I % 64 == 0, "down tiling");
@@ -184,7 +191,7 @@ int hmoe::dense_down(const _Float16* wd, const _Float16* act, int T, float* out,
                  "shared down: T %d or alignment", T);
     const dim3 g(H / BM, (T + BN - 1) / BN);
     constexpr int NT = 64 * DN_WM * DN_WN;
-    if (add) dgemm_kernel<1, DN_TM, DN_TN, DN_WM, DN_WN, DG_ADD><<<g, NT, 0, st>>>(wd, nullptr, act, T, I, out, H);
-    else dgemm_kernel<1, DN_TM, DN_TN, DN_WM, DN_WN, DG_D><<<g, NT, 0, st>>>(wd, nullptr, act, T, I, out, H);
+    if (mode == DG_MODE_ADD) dgemm_kernel<1, DN_TM, DN_TN, DN_WM, DN_WN, DG_ADD><<<g, NT, 0, st>>>(wd, nullptr, act, T, I, out, H);
+    else dgemm_kernel<1, DN_TM, DN_TN, DN_WM, DN_WN, DG_D16><<<g, NT, 0, st>>>(wd, nullptr, act, T, I, out, H);
     return HMOE_LAUNCHED("shared down");
 }
