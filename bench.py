@@ -58,9 +58,10 @@ def timed(torch, fn, steps, warmup):
     return time.perf_counter() - t0
 
 
-def timed_graph(torch, fn, steps, warmup):
+def timed_graph(torch, fn, steps, warmup, events=False):
     """the same steps captured in one hipGraph and replayed, as a decode loop runs its per-row-count step (the
-    reference captures its decode step once per row count, rtx_graph.py:6-8); the timed region is one replay"""
+    reference captures its decode step once per row count, rtx_graph.py:6-8); the timed region is one replay, timed
+    by the host clock around it or (events) by HIP events recorded on the launch stream"""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -70,10 +71,18 @@ def timed_graph(torch, fn, steps, warmup):
             fn(i)
     g.replay()                                          # (first replay uploads the graph)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    g.replay()
-    torch.cuda.synchronize()
-    el = time.perf_counter() - t0
+    if events:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        e1.synchronize()
+        el = e0.elapsed_time(e1) * 1e-3
+    else:
+        t0 = time.perf_counter()
+        g.replay()
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
     del g
     return el
 
@@ -99,17 +108,13 @@ def decode_workload(torch, synth, R, steps, warmup, zipf, dev, n_layers=6, n_x=6
     L, P = len(layers), len(xs)
     el_eager = timed(torch, lambda i: layers[i % L].decode(xs[i % P]), steps, warmup)
     el = timed_graph(torch, lambda i: layers[i % L].decode(xs[i % P]), steps, warmup)
-    # per-kernel timing of the same steps with HIP events on the launch stream: A (router logits), B (shared + routed
-    # gate/up + SwiGLU, gu7_kernel), C (shared + routed down, dn6_kernel), D (ordered reduce + bf16 out)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
-    for i in range(steps):
-        lay, x = layers[i % L], xs[i % P]
-        evs[i][0].record()
-        for k, ph in enumerate((1, 2, 4, 8)):
-            lay.decode(x, phases=ph)
-            evs[i][k + 1].record()
-    torch.cuda.synchronize()
-    kus = [float(np.mean([e[k].elapsed_time(e[k + 1]) for e in evs])) * 1e3 for k in range(4)]
+    # per-kernel timing of the same steps: each launch of the step (A router logits, B shared + routed gate/up +
+    # SwiGLU (gu7_kernel), C shared + routed down (dn6_kernel), D ordered reduce + bf16 out) repeated over the timed
+    # steps' layers and inputs in one hipGraph, timed with HIP events on the launch stream around its replay: the
+    # launch's duration in a decode loop, the step's other launches left out (single launches bracketed by events
+    # add the event and launch overhead to each)
+    kus = [timed_graph(torch, lambda i, ph=ph: layers[i % L].decode(xs[i % P], phases=ph), steps, 2, events=True)
+           / steps * 1e6 for ph in (1, 2, 4, 8)]
     # distinct experts of every timed step (deterministic: same layer / input pairs)
     U = []
     for i in range(steps):
