@@ -178,9 +178,9 @@ def partial_workload(torch, synth, steps, warmup, dev, n_layers=4):
         part = synth.gen_normal(synth.key(synth.SEED, 0, synth.KIND["PARTIAL"], R), R * H, dev, 0.0, 0.1).view(R, H)
 
         def step(i):
-            lay = layers[i % n_layers]
-            lay.route(xs[i % 32])
-            lay.experts_decode(R, part, with_shared=False)
+            # router logits, selection in the gate/up launch, the resident experts added into the partial: the four
+            # launches of the decode layer op with y and without the shared expert or the bf16 output
+            layers[i % n_layers].decode(xs[i % 32], y=part, out=False, with_shared=False)
         el_eager = timed(torch, step, steps, warmup)
         el = timed_graph(torch, step, steps, warmup)
         U = []

@@ -214,6 +214,15 @@ def test_partial_resident_176(dev, R):
     ma, mr = parity(y, ref)
     log(f"  max|d| {ma:.3e} mean-rel {mr:.3e}")
     assert ma <= MAX_ABS and mr <= MEAN_REL
+    # the same partial through the four launches of hmoe_moe_decode_layer (router logits, selection inside the gate/up
+    # launch, y accumulated, no shared expert, no bf16 out): the same selection and the same bound
+    yf = p0.clone()
+    assert lay.decode(x, y=yf, out=False, with_shared=False) is None
+    torch.cuda.synchronize()
+    assert np.array_equal(lay.sel[:R].cpu().numpy(), sel_ref)
+    ma, mr = parity(yf.cpu().numpy(), ref)
+    log(f"  fused layer op: max|d| {ma:.3e} mean-rel {mr:.3e}")
+    assert ma <= MAX_ABS and mr <= MEAN_REL
     # picks outside the window change nothing: all-absent selection leaves the partial as it was
     sel_out = torch.full((R, 8), 200, dtype=torch.int64, device=dev)
     lay.sel[:R].copy_(sel_out)
