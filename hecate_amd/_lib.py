@@ -40,6 +40,8 @@ SIGNATURES = {
     "hmoe_moe4p_scratch_bytes": (sz, [i32, i32, i32]),
     "hmoe_moe4p_forward": (i32, [P, P, P, P, P, i32, i32, i32, P, P, P, P, P, P, P, P, P, P, i32, P, P, i32, i32,
                                  P, P, P, i32, P]),
+    "hmoe_moe4p_forward_bf16": (i32, [P, P, P, P, P, i32, i32, i32, P, P, P, P, P, P, P, P, P, i32, P, P, i32, i32,
+                                      P, P, P, i32, P, P]),
     "hmoe_shared_work_bytes": (sz, [i32]),
     "hmoe_shared_forward": (i32, [P, i32, P, P, P, P, P, i32, P]),
     "hmoe_moe4t_scratch_bytes": (sz, [i32, i32]),

@@ -466,8 +466,11 @@ __global__ void __launch_bounds__(256) to_f16_kernel(const uint16_t* __restrict_
 // fin, deterministic: out[t] += (sum over k in top-k order of d[inv[t][k]]) (+ the shared expert's row), the d rows f16,
 // summed in fp32. Every row's load is unconditional (an absent pick or shared row reads row 0 and is dropped by a
 // select at its add), so all of them are in flight together: under a branch each load was followed by a wait for it.
+// OB: the sum goes to ob as bf16 (the partial out taken as zero and left untouched), as pfin into a zeroed out followed
+// by finish_bf16 (0 + s is s, and s is never -0: it starts at +0)
+template <bool OB>
 __global__ void __launch_bounds__(256) pfin_kernel(const _Float16* __restrict__ d, const int* __restrict__ inv, int topk,
-                                                   int np, int sh_off, float* __restrict__ out)
+                                                   int np, int sh_off, float* __restrict__ out, uint16_t* __restrict__ ob)
 {
     constexpr int NR = HMOE_TOPK + 1;
     const int t = blockIdx.x;
@@ -487,8 +490,6 @@ __global__ void __launch_bounds__(256) pfin_kernel(const _Float16* __restrict__ 
         f16x4 v[NR];
         #pragma unroll
         for (int k = 0; k < NR; ++k) v[k] = *(const f16x4*) (d + (size_t) pos[k] * H + n);
-        f32x4* o = (f32x4*) (out + (size_t) t * H + n);
-        const f32x4 ov = *o;
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
         #pragma unroll
         for (int k = 0; k < NR; ++k)
@@ -498,7 +499,18 @@ __global__ void __launch_bounds__(256) pfin_kernel(const _Float16* __restrict__ 
             for (int i = 0; i < 4; ++i) vk[i] = (float) v[k][i];
             s = use[k] ? s + vk : s;
         }
-        *o = ov + s;
+        if constexpr (OB)
+        {
+            uint32_t w[2];
+            #pragma unroll
+            for (int i = 0; i < 2; ++i) w[i] = (uint32_t) hmoe_f2bf(s[2 * i]) | ((uint32_t) hmoe_f2bf(s[2 * i + 1]) << 16);
+            *(uint2*) (ob + (size_t) t * H + n) = *(const uint2*) w;
+        }
+        else
+        {
+            f32x4* o = (f32x4*) (out + (size_t) t * H + n);
+            *o = *o + s;
+        }
     }
 }
 
@@ -554,16 +566,18 @@ extern "C" size_t hmoe_moe4p_scratch_bytes(int which, int ps, int T)
     }
 }
 
-extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid, const float* wt, const int* rbt,
-                                  int npos, int nrb, int n_tab, const int64_t* gw, const int64_t* uw, const int64_t* dw,
-                                  const int64_t* gs, const int64_t* us, const int64_t* ds, float* gu, uint16_t* ar,
-                                  float* d, float* out, int ps, const int* meta, const int* inv, int T, int topk,
-                                  const void* sh_gw, const void* sh_uw, const void* sh_dw, int xf, void* stream)
+// moe4p forward; ob (with inv): the combine writes bf16 rows to ob and out is neither read nor written
+static int moe4p_run(const void* x, const int* tok, const float* wt, const int* rbt, int npos, int nrb, int n_tab,
+                     const int64_t* gw, const int64_t* uw, const int64_t* dw, const int64_t* gs, const int64_t* us,
+                     const int64_t* ds, float* gu, uint16_t* ar, float* d, float* out, int ps, const int* meta,
+                     const int* inv, int T, int topk, const void* sh_gw, const void* sh_uw, const void* sh_dw, int xf,
+                     uint16_t* ob, void* stream)
 {
-    (void) eid;
     // an empty chunk is a no-op, as the reference returns when no pick reaches the tier (moe4p.cu:229)
     if (T == 0 && npos == 0) return HMOE_OK;
-    HMOE_REQUIRE(x && tok && wt && rbt && ar && d && out, "moe4p_forward: null buffer");
+    HMOE_REQUIRE(x && tok && wt && rbt && ar && d && (out || ob), "moe4p_forward: null buffer");
+    HMOE_REQUIRE(!ob || (inv && ((uintptr_t) ob & 7) == 0), "moe4p_forward_bf16: needs the inverse map and an 8-byte "
+                 "aligned bf16 output");
     HMOE_REQUIRE(npos >= 0 && nrb >= 0 && npos <= ps && T >= 1 && topk >= 1 && topk <= TOPK,
                  "moe4p_forward: npos %d nrb %d ps %d T %d topk %d", npos, nrb, ps, T, topk);
     // (the grouped GEMMs address their input rows by 32-bit byte offsets)
@@ -611,8 +625,34 @@ extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid,
                                 DG_MODE_F16, st))
             return rc;
     }
-    if (inv) pfin_kernel<<<T, 256, 0, st>>>((const _Float16*) d, inv, topk, npos, sh ? ps : -1, out);
+    if (inv && ob) pfin_kernel<true><<<T, 256, 0, st>>>((const _Float16*) d, inv, topk, npos, sh ? ps : -1, nullptr, ob);
+    else if (inv) pfin_kernel<false><<<T, 256, 0, st>>>((const _Float16*) d, inv, topk, npos, sh ? ps : -1, out, nullptr);
     return HMOE_LAUNCHED("moe4p_forward");
+}
+
+extern "C" int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid, const float* wt, const int* rbt,
+                                  int npos, int nrb, int n_tab, const int64_t* gw, const int64_t* uw, const int64_t* dw,
+                                  const int64_t* gs, const int64_t* us, const int64_t* ds, float* gu, uint16_t* ar,
+                                  float* d, float* out, int ps, const int* meta, const int* inv, int T, int topk,
+                                  const void* sh_gw, const void* sh_uw, const void* sh_dw, int xf, void* stream)
+{
+    (void) eid;
+    HMOE_REQUIRE(out || (T == 0 && npos == 0), "moe4p_forward: null buffer");
+    return moe4p_run(x, tok, wt, rbt, npos, nrb, n_tab, gw, uw, dw, gs, us, ds, gu, ar, d, out, ps, meta, inv, T, topk,
+                     sh_gw, sh_uw, sh_dw, xf, nullptr, stream);
+}
+
+extern "C" int hmoe_moe4p_forward_bf16(const void* x, const int* tok, const int* eid, const float* wt, const int* rbt,
+                                       int npos, int nrb, int n_tab, const int64_t* gw, const int64_t* uw,
+                                       const int64_t* dw, const int64_t* gs, const int64_t* us, const int64_t* ds,
+                                       float* gu, uint16_t* ar, float* d, int ps, const int* meta, const int* inv, int T,
+                                       int topk, const void* sh_gw, const void* sh_uw, const void* sh_dw, int xf,
+                                       uint16_t* out_bf16, void* stream)
+{
+    (void) eid;
+    HMOE_REQUIRE(out_bf16 || (T == 0 && npos == 0), "moe4p_forward_bf16: null buffer");
+    return moe4p_run(x, tok, wt, rbt, npos, nrb, n_tab, gw, uw, dw, gs, us, ds, gu, ar, d, nullptr, ps, meta, inv, T,
+                     topk, sh_gw, sh_uw, sh_dw, xf, out_bf16, stream);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -709,7 +749,7 @@ extern "C" int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid,
             pgemm_kernel<1, 2, 4, EPI_FIN, 16, 8><<<pgemm_grid(nrb, H / 256), 512, 0, st>>>((const _Float16*) ar, tok,
                 nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, nullptr, T, 0, npos, out);
     }
-    if (inv) pfin_kernel<<<T, 256, 0, st>>>((const _Float16*) d, inv, topk, npos, -1, out);
+    if (inv) pfin_kernel<false><<<T, 256, 0, st>>>((const _Float16*) d, inv, topk, npos, -1, out, nullptr);
     return HMOE_LAUNCHED("moe4t_forward");
 }
 

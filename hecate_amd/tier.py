@@ -331,8 +331,10 @@ class MoELayer:
                                   long=long)
         return self._pf
 
-    def prefill_experts(self, x, y, with_shared=True):
-        """routed (+ shared) experts of x's routed selection (in the prefill buffers) added into y fp32 [T, H]"""
+    def prefill_experts(self, x, y, with_shared=True, out_bf16=None):
+        """routed (+ shared) experts of x's routed selection (in the prefill buffers) added into y fp32 [T, H]; on the
+        moe4p path with out_bf16 (bf16 [T, H]) the sum is written there instead (y not touched, as if it were zero);
+        returns whether it was"""
         T = x.shape[0]
         pf = self._pf
         gq, uq, dq, gs, us, ds = self.bank.tables()
@@ -344,10 +346,12 @@ class MoELayer:
                           topk=self.topk)
             if with_shared and self.shared is not None:
                 moe4t.shared(x, *self.shared_rows(), pf.shw, y)
-            return
+            return False
         sh = self.shared_rows() if (with_shared and self.shared is not None) else None
-        moe4p.forward(x, pf.tok, pf.eid, pf.wt, pf.rbt, gq, uq, dq, gs, us, ds, *pf.scr, y,
-                      inv=pf.inv[:T * self.topk], meta=pf.meta, topk=self.topk, shared=sh, npos=pf.F, nrb=pf.nrb_max)
+        moe4p.forward(x, pf.tok, pf.eid, pf.wt, pf.rbt, gq, uq, dq, gs, us, ds, *pf.scr,
+                      y if out_bf16 is None else None, inv=pf.inv[:T * self.topk], meta=pf.meta, topk=self.topk,
+                      shared=sh, npos=pf.F, nrb=pf.nrb_max, out_bf16=out_bf16)
+        return out_bf16 is not None
 
     def shared_rows(self):
         """the shared expert as row-major f16 (gate [I, H], up [I, H], down [H, I]) for the prefill's dense GEMMs,
@@ -371,7 +375,9 @@ class MoELayer:
         router.router_fused(x, self.wg, self.bias, pf.logits, self.ctr, sel, rw, self.topk, self.scale, pf.xh[:T])
         pf.run(sel, rw, balance=True)
         y = pf.y[:T]
-        self.prefill_experts(pf.xh[:T], y, with_shared)
+        # (y is kept zeroed, so the moe4p path writes the bf16 output from its combine directly)
+        if self.prefill_experts(pf.xh[:T], y, with_shared, out_bf16=pf.out[:T]):
+            return pf.out[:T]
         return moe4.finish_bf16(y, T, pf.out[:T])
 
     def forward(self, x):

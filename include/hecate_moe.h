@@ -180,6 +180,14 @@ int hmoe_moe4p_forward(const void* x, const int* tok, const int* eid, const floa
                        const int64_t* us, const int64_t* ds, float* gu, uint16_t* ar, float* d, float* out, int ps,
                        const int* meta, const int* inv, int T, int topk, const void* sh_gw, const void* sh_uw,
                        const void* sh_dw, int xf, void* stream);
+/* No counterpart in the reference: hmoe_moe4p_forward into a zero partial followed by hmoe_finish_bf16, in one
+ * combine pass, for callers with no partial to add (the layer's own prefill). Arguments as hmoe_moe4p_forward without out; inv is required; out_bf16 bf16 [T][H] (8-byte aligned)
+ * gets bf16(sum of each token's picks in top-k order + shared row), bit-identical to the two-op form. */
+int hmoe_moe4p_forward_bf16(const void* x, const int* tok, const int* eid, const float* wt, const int* rbt, int npos,
+                            int nrb, int n_tab, const int64_t* gw, const int64_t* uw, const int64_t* dw,
+                            const int64_t* gs, const int64_t* us, const int64_t* ds, float* gu, uint16_t* ar, float* d,
+                            int ps, const int* meta, const int* inv, int T, int topk, const void* sh_gw,
+                            const void* sh_uw, const void* sh_dw, int xf, uint16_t* out_bf16, void* stream);
 
 /* ---- long prefill: runtime/tier/moe4/moe4t.cu:490-524 moe4t_scratch(device, npos) / moe4t_forward(x, tok, eid, wt,
  * rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out) ----

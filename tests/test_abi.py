@@ -59,6 +59,21 @@ def test_empty_prefill_chunk_is_a_no_op():
     assert L.hmoe_moe4p_forward(*args) != 0 and b"null" in L.hmoe_last_error()
 
 
+def test_prefill_bf16_output_entry_checks():
+    """hmoe_moe4p_forward_bf16 (the combine writing the bf16 output): an empty chunk is a no-op, and it refuses a
+    chunk without the inverse map (the per-token combine it needs) before any GPU call (the buffer addresses below
+    are never dereferenced)"""
+    L = _lib.lib()
+    args = [None] * 5 + [0, 0, 0] + [None] * 9 + [0, None, None, 0, 8, None, None, None, 0, None, None]
+    assert L.hmoe_moe4p_forward_bf16(*args) == 0
+    args[20] = 3
+    assert L.hmoe_moe4p_forward_bf16(*args) != 0 and b"null" in L.hmoe_last_error()
+    fake = 1 << 20
+    for i in (0, 1, 3, 4, 15, 16, 26):                      # x, tok, wt, rbt, ar, d, out_bf16
+        args[i] = fake
+    assert L.hmoe_moe4p_forward_bf16(*args) != 0 and b"inverse map" in L.hmoe_last_error()
+
+
 @pytest.mark.parametrize("N,K", [(16, 512), (64, 1536), (2048, 6144)])
 def test_pack_unpack_round_trip_and_layout(N, K):
     rng = np.random.default_rng(N)

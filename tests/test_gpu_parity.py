@@ -466,6 +466,15 @@ def test_prefill_parity(dev):
     y.zero_()
     torch.cuda.synchronize()
     check_all_rows(lay, hl, x, xn, yh, sel_ref, rw_ref)
+    # the layer's prefill writes its bf16 output from the combine (hmoe_moe4p_forward_bf16): bit-identical to the
+    # same sum into a zeroed fp32 partial rounded by finish_bf16, and the partial stays zeroed
+    out = lay.prefill(x).clone()
+    lay.prefill_experts(x, y)
+    out2 = torch.empty_like(out)
+    moe4.finish_bf16(y, T, out2)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+    assert not bool(y.any())
 
 
 def test_decode_bits_do_not_depend_on_the_grid(dev):
