@@ -47,6 +47,8 @@ SIGNATURES = {
     "hmoe_moe4t_scratch_bytes": (sz, [i32, i32]),
     "hmoe_moe4t_forward": (i32, [P, P, P, P, P, i32, i32, i32, P, P, P, P, P, P, P, P, P, P, i32, P, i32, i32, P, i32,
                                  P]),
+    "hmoe_moe4t_forward_bf16": (i32, [P, P, P, P, P, i32, i32, i32, P, P, P, P, P, P, P, P, P, P, i32, P, i32, i32, P,
+                                      i32, P, P]),
     "hmoe_moe4t_gemm": (i32, [P, i32, P, i32, i32, P, P, P, P, P, i32, i32, P]),
     "hmoe_residual_rmsnorm": (i32, [P, P, P, i32, f32, P, P, P]),
     "hmoe_norm_router": (i32, [P, P, f32, i32, P, i32, P, P, P, P]),

@@ -466,9 +466,11 @@ __global__ void __launch_bounds__(256) to_f16_kernel(const uint16_t* __restrict_
 // fin, deterministic: out[t] += (sum over k in top-k order of d[inv[t][k]]) (+ the shared expert's row), the d rows f16,
 // summed in fp32. Every row's load is unconditional (an absent pick or shared row reads row 0 and is dropped by a
 // select at its add), so all of them are in flight together: under a branch each load was followed by a wait for it.
-// OB: the sum goes to ob as bf16 (the partial out taken as zero and left untouched), as pfin into a zeroed out followed
-// by finish_bf16 (0 + s is s, and s is never -0: it starts at +0)
-template <bool OB>
+// MODE PF_ADD: out += the sum; PF_BF16: the sum goes to ob as bf16 (the partial out taken as zero and left untouched),
+// as PF_ADD into a zeroed out followed by finish_bf16 (0 + s is s, and s is never -0: it starts at +0); PF_FIN: ob =
+// bf16(out + sum) and out zeroed, as PF_ADD followed by finish_bf16
+enum { PF_ADD = 0, PF_BF16 = 1, PF_FIN = 2 };
+template <int MODE>
 __global__ void __launch_bounds__(256) pfin_kernel(const _Float16* __restrict__ d, const int* __restrict__ inv, int topk,
                                                    int np, int sh_off, float* __restrict__ out, uint16_t* __restrict__ ob)
 {
@@ -499,8 +501,14 @@ __global__ void __launch_bounds__(256) pfin_kernel(const _Float16* __restrict__ 
             for (int i = 0; i < 4; ++i) vk[i] = (float) v[k][i];
             s = use[k] ? s + vk : s;
         }
-        if constexpr (OB)
+        if constexpr (MODE != PF_ADD)
         {
+            if constexpr (MODE == PF_FIN)
+            {
+                f32x4* o = (f32x4*) (out + (size_t) t * H + n);
+                s = *o + s;
+                *o = (f32x4) {0.f, 0.f, 0.f, 0.f};
+            }
             uint32_t w[2];
             #pragma unroll
             for (int i = 0; i < 2; ++i) w[i] = (uint32_t) hmoe_f2bf(s[2 * i]) | ((uint32_t) hmoe_f2bf(s[2 * i + 1]) << 16);
@@ -625,8 +633,8 @@ static int moe4p_run(const void* x, const int* tok, const float* wt, const int* 
                                 DG_MODE_F16, st))
             return rc;
     }
-    if (inv && ob) pfin_kernel<true><<<T, 256, 0, st>>>((const _Float16*) d, inv, topk, npos, sh ? ps : -1, nullptr, ob);
-    else if (inv) pfin_kernel<false><<<T, 256, 0, st>>>((const _Float16*) d, inv, topk, npos, sh ? ps : -1, out, nullptr);
+    if (inv && ob) pfin_kernel<PF_BF16><<<T, 256, 0, st>>>((const _Float16*) d, inv, topk, npos, sh ? ps : -1, nullptr, ob);
+    else if (inv) pfin_kernel<PF_ADD><<<T, 256, 0, st>>>((const _Float16*) d, inv, topk, npos, sh ? ps : -1, out, nullptr);
     return HMOE_LAUNCHED("moe4p_forward");
 }
 
@@ -707,13 +715,12 @@ extern "C" size_t hmoe_moe4t_scratch_bytes(int which, int npos)
     }
 }
 
-extern "C" int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid, const float* wt, const int* rbt,
-                                  int npos, int nrb, int n_tab, const int64_t* gw, const int64_t* uw, const int64_t* dw,
-                                  const int64_t* gs, const int64_t* us, const int64_t* ds, float* gu, uint16_t* ar,
-                                  float* d, float* out, int ps, const int* meta, int T, int xf, const int* inv,
-                                  int topk, void* stream)
+// moe4t forward; ob (with inv): the combine writes bf16(out + picks) to ob and zeroes out
+static int moe4t_run(const void* x, const int* tok, const float* wt, const int* rbt, int npos, int nrb, int n_tab,
+                     const int64_t* gw, const int64_t* uw, const int64_t* dw, const int64_t* gs, const int64_t* us,
+                     const int64_t* ds, uint16_t* ar, float* d, float* out, int ps, const int* meta, int T, int xf,
+                     const int* inv, int topk, uint16_t* ob, void* stream)
 {
-    (void) eid; (void) gu;
     if (npos == 0) return HMOE_OK;                                      // moe4t.cu:508: no pick, no work
     HMOE_REQUIRE(x && tok && wt && rbt && ar && out, "moe4t_forward: null buffer");
     HMOE_REQUIRE(npos > 0 && nrb >= 0 && npos <= ps && T >= 1, "moe4t_forward: npos %d nrb %d ps %d T %d", npos, nrb, ps,
@@ -749,8 +756,35 @@ extern "C" int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid,
             pgemm_kernel<1, 2, 4, EPI_FIN, 16, 8><<<pgemm_grid(nrb, H / 256), 512, 0, st>>>((const _Float16*) ar, tok,
                 nullptr, rbt, nrb, meta, n_tab, dw, nullptr, ds, nullptr, nullptr, nullptr, T, 0, npos, out);
     }
-    if (inv) pfin_kernel<false><<<T, 256, 0, st>>>((const _Float16*) d, inv, topk, npos, -1, out, nullptr);
+    if (inv && ob) pfin_kernel<PF_FIN><<<T, 256, 0, st>>>((const _Float16*) d, inv, topk, npos, -1, out, ob);
+    else if (inv) pfin_kernel<PF_ADD><<<T, 256, 0, st>>>((const _Float16*) d, inv, topk, npos, -1, out, nullptr);
     return HMOE_LAUNCHED("moe4t_forward");
+}
+
+extern "C" int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid, const float* wt, const int* rbt,
+                                  int npos, int nrb, int n_tab, const int64_t* gw, const int64_t* uw, const int64_t* dw,
+                                  const int64_t* gs, const int64_t* us, const int64_t* ds, float* gu, uint16_t* ar,
+                                  float* d, float* out, int ps, const int* meta, int T, int xf, const int* inv,
+                                  int topk, void* stream)
+{
+    (void) eid; (void) gu;
+    return moe4t_run(x, tok, wt, rbt, npos, nrb, n_tab, gw, uw, dw, gs, us, ds, ar, d, out, ps, meta, T, xf, inv, topk,
+                     nullptr, stream);
+}
+
+extern "C" int hmoe_moe4t_forward_bf16(const void* x, const int* tok, const int* eid, const float* wt, const int* rbt,
+                                       int npos, int nrb, int n_tab, const int64_t* gw, const int64_t* uw,
+                                       const int64_t* dw, const int64_t* gs, const int64_t* us, const int64_t* ds,
+                                       float* gu, uint16_t* ar, float* d, float* out, int ps, const int* meta, int T,
+                                       int xf, const int* inv, int topk, uint16_t* out_bf16, void* stream)
+{
+    (void) eid; (void) gu;
+    HMOE_REQUIRE(out && out_bf16 && inv && T >= 1 && ((uintptr_t) out_bf16 & 7) == 0,
+                 "moe4t_forward_bf16: needs out, the inverse map and an 8-byte aligned bf16 output");
+    // no pick: the output is the partial alone (finish_bf16 rounds it and zeroes it)
+    if (npos == 0) return hmoe_finish_bf16(out, T, out_bf16, stream);
+    return moe4t_run(x, tok, wt, rbt, npos, nrb, n_tab, gw, uw, dw, gs, us, ds, ar, d, out, ps, meta, T, xf, inv, topk,
+                     out_bf16, stream);
 }
 
 extern "C" int hmoe_moe4t_gemm(const void* xs, int rows, const int* rbt, int nrb, int n_tab, const int64_t* w0,

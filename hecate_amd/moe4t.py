@@ -23,10 +23,11 @@ def scratch(dev, npos):
 
 
 def forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, meta=None, npos=None, nrb=None, inv=None,
-            topk=8):
+            topk=8, out_bf16=None):
     """moe4t.cu:498-524: out[tok] += routed experts of the sorted picks; x fp16 (as the reference) or bf16 [T, H].
     inv (the dispatch's inverse map, this build's addition): each token adds its picks in top-k order (deterministic)
-    instead of the down GEMM's atomic adds"""
+    instead of the down GEMM's atomic adds. out_bf16 (bf16 [T, H], with inv): the combine also rounds out to it and
+    zeroes out, as forward followed by moe4.finish_bf16 (hmoe_moe4t_forward_bf16)"""
     on_device("moe4t", x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, meta, inv)
     T = x.shape[0]
     if not (x.dim() == 2 and x.shape[1] == H and x.is_contiguous() and out.dtype == torch.float32
@@ -39,6 +40,15 @@ def forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, meta=N
     ps = ar.shape[0]
     if npos > ps or ar.shape[1] != I or ar.dtype != torch.float16 or d.numel() < ps * H or d.dtype != torch.float32:
         raise RuntimeError(f"moe4t: scratch for {ps} picks, {npos} given")
+    if out_bf16 is not None:
+        if inv is None or out_bf16.dtype != torch.bfloat16 or not out_bf16.is_contiguous() \
+                or tuple(out_bf16.shape) != (T, H):
+            raise RuntimeError("moe4t: out_bf16 (bf16 [T, H]) needs the inverse map")
+        on_device("moe4t", out_bf16)
+        call("hmoe_moe4t_forward_bf16", ptr(x), ptr(tok), ptr(eid), ptr(wt), ptr(rbt), npos, nrb, gw.numel(), ptr(gw),
+             ptr(uw), ptr(dw), ptr(gs), ptr(us), ptr(ds), ptr(gu), ptr(ar), ptr(d), ptr(out), ps, ptr(meta), T,
+             xf_of(x), ptr(inv), int(topk), ptr(out_bf16), stream_of(x.device))
+        return
     call("hmoe_moe4t_forward", ptr(x), ptr(tok), ptr(eid), ptr(wt), ptr(rbt), npos, nrb, gw.numel(), ptr(gw),
          ptr(uw), ptr(dw), ptr(gs), ptr(us), ptr(ds), ptr(gu), ptr(ar), ptr(d), ptr(out), ps, ptr(meta), T, xf_of(x),
          ptr(inv), int(topk), stream_of(x.device))

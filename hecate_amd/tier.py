@@ -332,21 +332,26 @@ class MoELayer:
         return self._pf
 
     def prefill_experts(self, x, y, with_shared=True, out_bf16=None):
-        """routed (+ shared) experts of x's routed selection (in the prefill buffers) added into y fp32 [T, H]; on the
-        moe4p path with out_bf16 (bf16 [T, H]) the sum is written there instead (y not touched, as if it were zero);
+        """routed (+ shared) experts of x's routed selection (in the prefill buffers) added into y fp32 [T, H]; with
+        out_bf16 (bf16 [T, H]) the layer output bf16(y + experts) is written there instead and y left zeroed (moe4p:
+        y, kept zeroed, is not touched; moe4t with the ordered combine: y is rounded and re-zeroed by the combine);
         returns whether it was"""
         T = x.shape[0]
         pf = self._pf
         gq, uq, dq, gs, us, ds = self.bank.tables()
         if pf.long:
             # tier_split.py:427-462: every routed expert on moe4t (256-pick balanced blocks, the down GEMM adding into
-            # y), the shared expert apart
+            # y), the shared expert apart. With out_bf16 and the ordered combine, the shared expert goes into y first
+            # and the combine rounds y + picks to out_bf16 (y + s equals s + y bit for bit) and re-zeroes y
+            fused = out_bf16 is not None and self.deterministic
+            if fused and with_shared and self.shared is not None:
+                moe4t.shared(x, *self.shared_rows(), pf.shw, y)
             moe4t.forward(x, pf.tok, pf.eid, pf.wt, pf.rbt, gq, uq, dq, gs, us, ds, *pf.scr, y, meta=pf.meta,
                           npos=pf.F, nrb=pf.nrb_max, inv=pf.inv[:T * self.topk] if self.deterministic else None,
-                          topk=self.topk)
-            if with_shared and self.shared is not None:
+                          topk=self.topk, out_bf16=out_bf16 if fused else None)
+            if not fused and with_shared and self.shared is not None:
                 moe4t.shared(x, *self.shared_rows(), pf.shw, y)
-            return False
+            return fused
         sh = self.shared_rows() if (with_shared and self.shared is not None) else None
         moe4p.forward(x, pf.tok, pf.eid, pf.wt, pf.rbt, gq, uq, dq, gs, us, ds, *pf.scr,
                       y if out_bf16 is None else None, inv=pf.inv[:T * self.topk], meta=pf.meta, topk=self.topk,

@@ -206,6 +206,15 @@ int hmoe_moe4t_forward(const void* x, const int* tok, const int* eid, const floa
                        int nrb, int n_tab, const int64_t* gw, const int64_t* uw, const int64_t* dw, const int64_t* gs,
                        const int64_t* us, const int64_t* ds, float* gu, uint16_t* ar, float* d, float* out, int ps,
                        const int* meta, int T, int xf, const int* inv, int topk, void* stream);
+/* No counterpart in the reference: hmoe_moe4t_forward (with inv) followed by hmoe_finish_bf16, in one combine pass:
+ * out_bf16 bf16 [T][H] (8-byte aligned) = bf16(out + each token's picks in top-k order) and out zeroed, bit-identical
+ * to the two-op form; npos = 0 gives finish_bf16 of out alone. For the layer's long prefill (the shared expert added
+ * into out first). */
+int hmoe_moe4t_forward_bf16(const void* x, const int* tok, const int* eid, const float* wt, const int* rbt, int npos,
+                            int nrb, int n_tab, const int64_t* gw, const int64_t* uw, const int64_t* dw,
+                            const int64_t* gs, const int64_t* us, const int64_t* ds, float* gu, uint16_t* ar, float* d,
+                            float* out, int ps, const int* meta, int T, int xf, const int* inv, int topk,
+                            uint16_t* out_bf16, void* stream);
 /* runtime/tier/moe4/moe4t.cu:476-488 moe4t_gemm(xs, rbt, w0, w1, out, down), the test entry: one grouped GEMM over
  * row blocks of <= 256 picks whose inputs are rows p of xs f16 [rows][K]. Gate/up shape (down = 0, K = H): out fp32
  * [2][ps][I] = the gate (w0, s0) and up (w1, s1) sums; down shape (down = 1, K = I): out fp32 [ps][H] (w0, s0). The

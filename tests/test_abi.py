@@ -72,6 +72,9 @@ def test_prefill_bf16_output_entry_checks():
     for i in (0, 1, 3, 4, 15, 16, 26):                      # x, tok, wt, rbt, ar, d, out_bf16
         args[i] = fake
     assert L.hmoe_moe4p_forward_bf16(*args) != 0 and b"inverse map" in L.hmoe_last_error()
+    # the long-prefill form: the inverse map and the partial are required (checked before any GPU call)
+    targs = [None] * 5 + [0, 0, 0] + [None] * 10 + [0, None, 3, 0, None, 8, None, None]
+    assert L.hmoe_moe4t_forward_bf16(*targs) != 0 and b"inverse map" in L.hmoe_last_error()
 
 
 @pytest.mark.parametrize("N,K", [(16, 512), (64, 1536), (2048, 6144)])

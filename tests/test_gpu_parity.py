@@ -633,6 +633,15 @@ def test_long_prefill_moe4t(dev, T, ordered):
     yh = y.cpu().numpy()
     y.zero_()
     torch.cuda.synchronize()
+    if ordered:
+        # the layer's output comes from the combine itself (hmoe_moe4t_forward_bf16, the shared expert added into the
+        # partial first): bit-identical to the two-op form's fp32 sum rounded by finish_bf16, and the partial re-zeroed
+        y2 = torch.from_numpy(yh).to(dev)
+        o2 = torch.empty_like(out)
+        moe4.finish_bf16(y2, T, o2)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), o2.view(torch.int16))
+        assert not bool(pf.y[:T].any())
     # (the atomic adds make the last bits of a run order-dependent: bf16 out within one ulp of this run's rounding)
     ob = O.bf16_to_f32(u16(out))
     assert np.abs(ob - O.bf16_to_f32(O.f32_to_bf16(yh))).max() <= 2 ** -7 * max(np.abs(yh).max(), 1.0)
