@@ -109,12 +109,14 @@ def decode_workload(torch, synth, R, steps, warmup, zipf, dev, n_layers=6, n_x=6
     el_eager = timed(torch, lambda i: layers[i % L].decode(xs[i % P]), steps, warmup)
     el = timed_graph(torch, lambda i: layers[i % L].decode(xs[i % P]), steps, warmup)
     # per-kernel timing of the same steps: each launch of the step (A router logits, B shared + routed gate/up +
-    # SwiGLU (gu7_kernel), C shared + routed down (dn6_kernel), D ordered reduce + bf16 out) repeated over the timed
-    # steps' layers and inputs in one hipGraph, timed with HIP events on the launch stream around its replay: the
-    # launch's duration in a decode loop, the step's other launches left out (single launches bracketed by events
-    # add the event and launch overhead to each)
+    # SwiGLU (gu7_kernel), C shared + routed down (at one row dn8_kernel, which also adds the parts in order and
+    # writes the bf16 out; above, dn6_kernel's part partials), D the ordered reduce + bf16 out of the part form (no
+    # launch at one row)) repeated over the timed steps' layers and inputs in one hipGraph, timed with HIP events on
+    # the launch stream around its replay: the launch's duration in a decode loop, the step's other launches left out
+    # (single launches bracketed by events add the event and launch overhead to each)
+    own = R == 1
     kus = [timed_graph(torch, lambda i, ph=ph: layers[i % L].decode(xs[i % P], phases=ph), steps, 2, events=True)
-           / steps * 1e6 for ph in (1, 2, 4, 8)]
+           / steps * 1e6 if not (own and ph == 8) else 0.0 for ph in (1, 2, 4, 8)]
     # distinct experts of every timed step (deterministic: same layer / input pairs)
     U = []
     for i in range(steps):
@@ -128,14 +130,14 @@ def decode_workload(torch, synth, R, steps, warmup, zipf, dev, n_layers=6, n_x=6
               float(np.mean(U * GU_EXPERT_BYTES + SHARED_GU_BYTES + R * H * 2)),
               float(np.mean(U * DOWN_EXPERT_BYTES + SHARED_DOWN_BYTES + (U + 1) * R * 2048 * 2)),
               0.0]
-    names = ["A_router", "B_gate_up", "C_down", "D_reduce_out"]
+    names = ["A_router", "B_gate_up", "C_down_out" if own else "C_down", "D_reduce_out"]
     res = {"rows": R, "us_per_step": step_s * 1e6, "us_per_step_eager": el_eager / steps * 1e6,
            "us_per_token": step_s * 1e6 / R, "tok_per_s": R / step_s,
            "distinct_experts_mean": float(U.mean()), "bytes_per_step": bytes_step,
            "hbm_gbs": bytes_step / step_s / 1e9, "hbm_frac": bytes_step / step_s / 1e9 / HBM_PEAK_GBS,
            "kernels": {n: {"us": kus[k], "algorithmic_bytes": kbytes[k],
                            "gbs": kbytes[k] / (kus[k] * 1e-6) / 1e9 if kbytes[k] else None}
-                       for k, n in enumerate(names)}}
+                       for k, n in enumerate(names) if not (own and k == 3)}}
     del layers, xs
     torch.cuda.empty_cache()
     return res

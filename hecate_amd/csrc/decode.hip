@@ -675,6 +675,201 @@ __global__ void __launch_bounds__(DW * 64) dn6_kernel(
     }
 }
 
+// ---- down for one row: output rows owned, no part buffer and no reduction launch ----
+// Workgroup b owns the 24 output rows [24 b, 24 b + 24): one whole 16-row tile (nbF) and one half tile (rows
+// 8 ph .. 8 ph + 8 of tile nbH), so 256 workgroups cover H with equal work. It runs every part of the step for those
+// rows, the shared expert (part 0) and each slot quad, with the waves in dn6_kernel's roles (routed: slot w / 4 of the
+// quad, k quarter w % 4; shared: k group w), the same MFMA chains and the same wave-ordered part sums, and adds the
+// parts in order into one fp32 sum per output: the bits of dn6_kernel followed by dec_d_kernel. The half tile's loads
+// let lanes l and l ^ 8 read the same 16 bytes (its 8 rows, whole 128-byte lines); its MFMA columns of the other half
+// are duplicates, never stored. A quad item runs as two sub-items of 2 k groups.
+// At one row a step has at most 8 distinct experts (2 slot quads, 4 sub-items per wave), so nothing needs a ring:
+// each wave issues its shared tiles, then (after the pointer tables) its first two routed sub-items, and the last two
+// as soon as the shared tiles' registers are free. The act rows of the 8 slots (32 KB) and the shared act go to LDS at
+// the start (their loads are issued ahead of every tile), so no act load waits behind a tile. The MFMA A rows of
+// tokens past row 0 read row 0 again: those output rows are never stored, and MFMA rows do not interact.
+// (With more rows the act of a step no longer fits LDS, and a variant of this kernel holding each quad's act in
+// registers could keep too few tiles in flight: 16 waves at 128 registers each; it measured slower than the part-sum
+// form at 4 rows, so rows past the first take that form.)
+constexpr int DN8_GRID = H / 24;                      // 256 workgroups of 24 rows
+
+template <bool SH>
+__global__ void __launch_bounds__(DW * 64) dn8_kernel(
+    int n_hot, const int64_t* __restrict__ down_w, const int64_t* __restrict__ down_s,
+    const _Float16* __restrict__ act, const uint8_t* __restrict__ sh_dw, float* __restrict__ y,
+    uint16_t* __restrict__ out)
+{
+    constexpr int XL = I + 8;                                   // LDS row stride (f16) of an act row
+    constexpr int O_RED = 0, O_TAB = O_RED + 2 * DW * 2 * 64 * 16, O_PTR = O_TAB + 2 * HMOE_MAXE * 8;
+    constexpr int O_ACT = O_PTR + 2 * MAXSLOT * 8, O_XSH = O_ACT + 8 * XL * 2, N_SMEM = O_XSH + XL * 2;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[N_SMEM];
+    auto& tab = *reinterpret_cast<const uint8_t* (*)[2][HMOE_MAXE]>(smem + O_TAB);
+    auto& ptr = *reinterpret_cast<const uint8_t* (*)[2][MAXSLOT]>(smem + O_PTR);
+    auto& red = *reinterpret_cast<f32x4 (*)[2][DW][2][64]>(smem + O_RED);
+    auto& act8 = *reinterpret_cast<_Float16 (*)[8][XL]>(smem + O_ACT);
+    auto& xsh = *reinterpret_cast<_Float16 (*)[XL]>(smem + O_XSH);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int sw = w >> 2, kq = w & 3;
+    const int b = blockIdx.x;
+    const int ph = b & 1;
+    const int nbF = (3 * b + ph) >> 1, nbH = ph ? nbF - 1 : nbF + 1;
+    const int lh = (l & ~8) | (ph << 3);
+    asm volatile("" :: "s"(sh_dw), "s"(out));
+    const int te = min((int) threadIdx.x, max(n_hot - 1, 0));
+    const int* rec = (const int*) (act + (size_t) REC_SLOT * MAXR * I);
+    const int64_t t0 = ldg<int64_t>(n_hot > 0 ? down_w + te : (const int64_t*) rec);
+    const int64_t t1 = ldg<int64_t>(n_hot > 0 ? down_s + te : (const int64_t*) rec);
+    const int re = ldg<int>(rec + REC_E + min((int) threadIdx.x, MAXSLOT - 1));
+    // row 0 of act slots 0..7 (2 pieces of 8 f16 per thread; slots past m hold stale values, never used)
+    u32x4 av[2];
+    #pragma unroll
+    for (int c = 0; c < 2; ++c)
+    {
+        const int p = (int) threadIdx.x + DW * 64 * c;
+        av[c] = ld16(act + (size_t) (p >> 8) * MAXR * I + (p & 255) * 8);
+    }
+    u32x4 gv = {}, uv = {};
+    if (SH)
+    {
+        const float* shp = (const float*) (act + (size_t) SHP_SLOT * MAXR * I);
+        const int q = min((int) threadIdx.x, I / 4 - 1);
+        gv = ld16(shp + q * 4);
+        uv = ld16(shp + MAXR * I + q * 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 SF[4], SH4[4];
+    if (SH)
+    {
+        const uint8_t* wf = sh_dw + ((size_t) (nbF * KS_I + 4 * w) * 64 + l) * 16;
+        const uint8_t* wh = sh_dw + ((size_t) (nbH * KS_I + 4 * w) * 64 + lh) * 16;
+        #pragma unroll
+        for (int k = 0; k < 4; ++k) SF[k] = ldw16(wf + k * 1024);
+        #pragma unroll
+        for (int k = 0; k < 4; ++k) SH4[k] = ldw16(wh + k * 1024);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    #pragma unroll
+    for (int c = 0; c < 2; ++c)
+    {
+        const int p = (int) threadIdx.x + DW * 64 * c;
+        *(u32x4*) &act8[p >> 8][(p & 255) * 8] = av[c];
+    }
+    if (SH && threadIdx.x < I / 4)
+    {
+        f16x4 v;
+        #pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (_Float16) (silu(__uint_as_float(gv[e])) * __uint_as_float(uv[e]));
+        *(f16x4*) &xsh[threadIdx.x * 4] = v;
+    }
+    tab[0][te] = (const uint8_t*) t0; tab[1][te] = (const uint8_t*) t1;
+    __syncthreads();
+    const int m = min(max(__builtin_amdgcn_readfirstlane(re) >> 16, 0), min(n_hot, 8)), nq = (m + 3) / 4;
+    if (threadIdx.x < m)
+    {
+        const int e = min(re & 0xffff, n_hot - 1);
+        ptr[0][threadIdx.x] = tab[0][e]; ptr[1][threadIdx.x] = tab[1][e];
+    }
+    if (m == 0 && threadIdx.x == 0) { ptr[0][0] = (const uint8_t*) act; ptr[1][0] = (const uint8_t*) act; }
+    __syncthreads();
+    // reducing threads: thread o < 24 owns output row 24 b + o (token 0, element 0 of its lane)
+    const int o = threadIdx.x;
+    const bool ored = o < 24;
+    const int on = 24 * b + o, of = (on >> 4) == nbF ? 0 : 1, oll = on & 15;
+    float s = 0.f;
+    auto reduce = [&](const f32x4& af, const f32x4& ah, int par) {
+        red[par][w][0][l] = af; red[par][w][1][l] = ah;
+        __syncthreads();
+        if (ored)
+        {
+            float sum = 0.f;
+            #pragma unroll
+            for (int ww = 0; ww < DW; ++ww) sum += red[par][ww][of][oll][0];
+            s = s + sum;
+        }
+    };
+    const DqConsts dq = dq_consts();
+    struct Sub { u32x4 f[2], h[2]; uint32_t sf, shh; };
+    const int nsub = 2 * nq;
+    auto load = [&](Sub& S, int i) {
+        const int qd = i >> 1, hf = i & 1, j = 4 * qd + sw;
+        const int jj = max(min(j, m - 1), 0);
+        const int g0 = 4 * kq + 2 * hf;
+        const size_t tf = (uint32_t) (((nbF * KG_I + g0) * 64 + l) * 16);
+        const size_t th = (uint32_t) (((nbH * KG_I + g0) * 64 + lh) * 16);
+        const size_t sf = (uint32_t) (sc_index(nbF * 16 + (l & 15), g0, KG_I) * 2);
+        const size_t sh = (uint32_t) (sc_index(nbH * 16 + (lh & 15), g0, KG_I) * 2);
+        const int kst = (j < m && i < nsub) ? 1024 : 0;
+        #pragma unroll
+        for (int k = 0; k < 2; ++k)
+        {
+            S.f[k] = ldw16(ptr[0][jj] + tf + k * kst);
+            S.h[k] = ldw16(ptr[0][jj] + th + k * kst);
+        }
+        S.sf = ldg<uint32_t>(ptr[1][jj] + sf);
+        S.shh = ldg<uint32_t>(ptr[1][jj] + sh);
+    };
+    Sub S0, S1, S2, S3;
+    load(S0, 0);
+    load(S1, 1);
+    f32x4 af = {0.f, 0.f, 0.f, 0.f}, ah = af;
+    int par = 0;
+    // the A fragments of k group g of a 512-k range starting at k0 in an LDS act row (every lane reads the row)
+    auto frag = [&](const _Float16* rowp, int k0, int g, f16x8 (&xa)[4]) {
+        #pragma unroll
+        for (int t = 0; t < 4; ++t) xa[t] = *(const f16x8*) (rowp + k0 + 128 * g + 32 * t + 8 * (l >> 4));
+    };
+    if (SH)
+    {
+        f16x8 xs[4];
+        frag(&xsh[0], 128 * w, 0, xs);
+        #pragma unroll
+        for (int t = 0; t < 4; ++t) af = mfma16(xs[t], as_f16x8(SF[t]), af);
+        #pragma unroll
+        for (int t = 0; t < 4; ++t) ah = mfma16(xs[t], as_f16x8(SH4[t]), ah);
+        reduce(af, ah, 0);
+        par = 1;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load(S2, 2);
+    load(S3, 3);
+    __builtin_amdgcn_sched_barrier(0);
+    auto scale2 = [](uint32_t v, int k) { return __uint_as_float(k ? (v & 0xffff0000u) : (v << 16)); };
+    auto run = [&](const Sub& S, int qd, auto hfc) {
+        constexpr int HF = decltype(hfc)::value;
+        if (HF == 0) { af = (f32x4) {0.f, 0.f, 0.f, 0.f}; ah = af; }
+        const _Float16* rowp = &act8[min(4 * qd + sw, 7)][0];
+        #pragma unroll
+        for (int k = 0; k < 2; ++k)
+        {
+            f16x8 xa[4];
+            frag(rowp, 512 * kq, 2 * HF + k, xa);
+            group_i4(xa, S.f[k], scale2(S.sf, k), af, dq);
+            group_i4(xa, S.h[k], scale2(S.shh, k), ah, dq);
+        }
+        if (HF == 1)
+        {
+            if (4 * qd + sw >= m) { af = (f32x4) {0.f, 0.f, 0.f, 0.f}; ah = af; }
+            reduce(af, ah, par);
+            par ^= 1;
+        }
+    };
+    if (nq > 0)
+    {
+        run(S0, 0, ic<0>{});
+        run(S1, 0, ic<1>{});
+    }
+    if (nq > 1)
+    {
+        run(S2, 1, ic<0>{});
+        run(S3, 1, ic<1>{});
+    }
+    if (ored)
+    {
+        if (y) y[on] = y[on] + s;
+        if (out) out[on] = hmoe_f2bf(s);
+    }
+}
+
 // ---- y (+)= sum of the parts in order; or the layer's bf16 output ----
 // one thread per element: the parts are loaded 8 at a time (the first 8 before the part count arrives; a part past the
 // count is read, from inside the buffer, and not added), then added in part order
@@ -748,8 +943,10 @@ static int check(const DecodeArgs& a)
 }
 
 // launches; phase mask bit 0 = router logits, 1 = shared + routed gate/up, 2 = shared + routed down, 3 = ordered
-// reduction. blocks: grid of the gate/up and down kernels (0 = one workgroup per CU); with the shared expert the
-// gate/up grid is GU_SH_GRID (one shared matrix slice each) and the down grid is kept in [DN_GMIN, DN_GMAX].
+// reduction (nothing to do after the owning down form of one row); bit 4 takes the part-sum down form
+// (down, then reduction) at any row count. blocks: grid of the gate/up and down kernels (0 = one workgroup per CU);
+// with the shared expert the gate/up grid is GU_SH_GRID (one shared matrix slice each) and the part-sum down grid is
+// kept in [DN_GMIN, DN_GMAX].
 static int run_decode(const DecodeArgs& a, int phases, hipStream_t st)
 {
     const int R = a.R;
@@ -771,7 +968,18 @@ static int run_decode(const DecodeArgs& a, int phases, hipStream_t st)
                                                      a.lo, a.n_hot, a.gate_w, a.up_w, a.gate_s, a.up_s, nullptr,
                                                      nullptr, a.act, G);
     }
-    if (phases & 4)
+    // at one row the down launch owns its output rows and writes y / out itself (no part buffer, no reduction
+    // launch: phase 8 has nothing left to do); more rows take the part-sum form (down, then reduce)
+    const bool own = R == 1 && !(phases & 16);
+    if ((phases & 4) && own)
+    {
+        if (sh)
+            dn8_kernel<true><<<DN8_GRID, DW * 64, 0, st>>>(a.n_hot, a.down_w, a.down_s, a.act, (const uint8_t*) a.sh_dw,
+                                                           a.y, a.out);
+        else
+            dn8_kernel<false><<<DN8_GRID, DW * 64, 0, st>>>(a.n_hot, a.down_w, a.down_s, a.act, nullptr, a.y, a.out);
+    }
+    if ((phases & 4) && !own)
     {
         const int gd = min(max(G, DN_GMIN), DN_GMAX);
         if (sh)
@@ -785,7 +993,7 @@ static int run_decode(const DecodeArgs& a, int phases, hipStream_t st)
             dn6_kernel<false, 1><<<gd, DW * 64, 0, st>>>(R, a.n_hot, a.down_w, a.down_s, a.act, nullptr, a.y32, a.ctr,
                                                          gd);
     }
-    if (phases & 8) dec_d_kernel<<<(R * H + 255) / 256, 256, 0, st>>>(a.y32, a.ctr, R, a.y, a.out);
+    if ((phases & 8) && !own) dec_d_kernel<<<(R * H + 255) / 256, 256, 0, st>>>(a.y32, a.ctr, R, a.y, a.out);
     return HMOE_LAUNCHED("moe4");
 }
 
@@ -945,7 +1153,7 @@ extern "C" int hmoe_moe_decode_layer(const void* x, const float* wt, const float
     HMOE_REQUIRE(wt && logits && sel && rw && E >= TOPK && E <= RMAXE && topk == TOPK && ((uintptr_t) wt & 15) == 0,
                  "decode_layer: router arguments");
     HMOE_REQUIRE(y || out, "decode_layer: no output");
-    HMOE_REQUIRE(phases >= 1 && phases <= 15, "decode_layer: phases %d", phases);
+    HMOE_REQUIRE(phases >= 1 && phases <= 31 && (phases & 15), "decode_layer: phases %d", phases);
     DecodeArgs a = forward_args(x, nullptr, nullptr, R, n_hot, gate_w, up_w, down_w, gate_s, up_s, down_s, act, ctr_a,
                                 y32, y, blocks, lo, sh_gw, sh_uw, sh_dw, HMOE_XF_BF16);
     a.wt = wt; a.bias = bias; a.logits = logits; a.E = E; a.topk = topk; a.scale = scale; a.sel_out = sel;

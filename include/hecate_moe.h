@@ -116,9 +116,10 @@ int hmoe_moe4_forward_noalloc(const void* x, const int64_t* sel, const uint16_t*
                               const void* sh_gw, const void* sh_uw, const void* sh_dw, int xf, void* stream);
 /* the two phases of hmoe_moe4_forward, for callers that time or schedule them apart (this build's addition):
  * gate_up writes act (with the shared expert: also its fp32 gate and up sums, in act) and, in act, the step's routing
- * record (distinct expert count and the local expert of each act slot); down adds into y (ctr_b carries its part
- * count), taking the slots from that record, so it must follow a gate_up of the same step on the same act (sel, rw
- * and lo are accepted for the argument positions); same arguments and rules as forward otherwise */
+ * record (distinct expert count and the local expert of each act slot); down adds into y (above one row ctr_b
+ * carries its part count to the ordered sum), taking the slots from that record, so it must follow a gate_up of the
+ * same step on the same act (sel, rw and lo are accepted for the argument positions); same arguments and rules as
+ * forward otherwise */
 int hmoe_moe4_gate_up(const void* x, const int64_t* sel, const uint16_t* rw, int R, int n_hot,
                       const int64_t* gate_w, const int64_t* up_w, const int64_t* gate_s, const int64_t* up_s,
                       void* act, float* gu32, int* ctr_a, int blocks, int lo, const void* sh_gw, const void* sh_uw,
@@ -131,7 +132,10 @@ int hmoe_moe4_down(const int64_t* sel, const uint16_t* rw, int R, int n_hot, con
  * selection written to sel / rw (int64 / f16 [R][8]), routed experts of the picks in [lo, lo + n_hot) and the shared
  * expert (F16T or NULL); y fp32 [R][H] accumulated into and / or out bf16 [R][H] written (either may be NULL, not
  * both). x bf16 [R][H]. phases: bit mask of the four launches (1 router logits, 2 selection + shared and routed
- * gate/up, 4 shared and routed down, 8 output), 15 = the whole layer. topk must be 8. */
+ * gate/up, 4 shared and routed down, 8 output), 15 = the whole layer. At one row the down launch owns its output
+ * rows and writes y / out itself (the layer is three launches; bit 8 then launches nothing); bit 16 takes the
+ * part-sum form (down partials, then the ordered output launch) at any row count, with the same bits. topk must
+ * be 8. */
 int hmoe_moe_decode_layer(const void* x, const float* wt, const float* bias, int E, int topk, float scale,
                           float* logits, int64_t* sel, uint16_t* rw, int R, int n_hot, int lo,
                           const int64_t* gate_w, const int64_t* up_w, const int64_t* down_w,

@@ -488,6 +488,25 @@ def test_decode_bits_do_not_depend_on_the_grid(dev):
         assert all(torch.equal(outs[0], o) for o in outs[1:]), R
 
 
+@pytest.mark.parametrize("R", [1])
+def test_owning_down_matches_part_sums(dev, R):
+    """at one row the down launch owns 24 output rows per workgroup and adds the parts (shared expert, then each slot
+    quad) in order itself; the part-sum form (phases bit 16: down partials, then the ordered output launch) gives the
+    same bits, for y accumulated into a non-zero start and for the bf16 out, with and without the shared expert"""
+    log(f"owning down R={R}")
+    lay = gpu_layer("c0", dev, layer=0)
+    x = synth.gen_x(60 + R, R, dev)
+    y0 = synth.gen_normal(synth.key(synth.SEED, 0, synth.KIND["PARTIAL"], R), R * H, dev, 0.0, 0.1).view(R, H)
+    for with_shared in (True, False):
+        ya, yb = y0.clone(), y0.clone()
+        oa = lay.decode(x, y=ya, with_shared=with_shared).clone()
+        ob = lay.decode(x, y=yb, with_shared=with_shared, phases=31).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(ya.view(torch.int32), yb.view(torch.int32)), with_shared
+        assert torch.equal(oa.view(torch.int16), ob.view(torch.int16)), with_shared
+        assert not torch.equal(ya, y0)
+
+
 def test_prefill_empty_and_no_picks(dev):
     """the reference's early returns (moe4p.cu:229 when no pick reaches the tier, tier_split.py:377): an empty chunk
     gives an empty output without an error, and a call with no picks and no shared expert leaves out untouched"""
