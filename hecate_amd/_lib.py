@@ -51,6 +51,10 @@ SIGNATURES = {
                                       i32, P, P]),
     "hmoe_moe4t_gemm": (i32, [P, i32, P, i32, i32, P, P, P, P, P, i32, i32, P]),
     "hmoe_residual_rmsnorm": (i32, [P, P, P, i32, f32, P, P, P]),
+    "hmoe_combine_norm": (i32, [P, P, P, i32, P, P, P, P, P, f32, f32, f32, i32, i32, P]),
+    "hmoe_norm_route_scratch_bytes": (sz, [i32, i32]),
+    "hmoe_norm_route": (i32, [P, P, P, P, P, P, P, P, P, P, f32, f32, f32, f32, P, i32, i32, i32, i32, i32, i32, P]),
+    "hmoe_decode_combine_norm": (i32, [P, P, i32, P, P, P, P, f32, f32, f32, i32, i32, P]),
     "hmoe_norm_router": (i32, [P, P, f32, i32, P, i32, P, P, P, P]),
     "hmoe_cpu_start": (i32, [P, i32, i32]),
     "hmoe_cpu_add_layer": (i32, [i32, i32, i32, P, P]),
@@ -129,3 +133,14 @@ def xf_of(x, xf=0):
 def stream_of(device=None):
     import torch
     return torch.cuda.current_stream(device).cuda_stream
+
+
+DT_F32, DT_BF16, DT_F16 = 0, 1, 2       # the dtype codes of include/hecate_moe.h (HMOE_DT_*)
+
+
+def dt_of(t, allowed=("float32", "bfloat16", "float16")):
+    """the C ABI's dtype code of a torch tensor (RuntimeError for a dtype the entry does not take)"""
+    name = str(t.dtype).replace("torch.", "")
+    if name not in allowed:
+        raise RuntimeError(f"dtype {t.dtype} not supported here ({', '.join(allowed)})")
+    return {"float32": DT_F32, "bfloat16": DT_BF16, "float16": DT_F16}[name]

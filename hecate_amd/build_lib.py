@@ -12,7 +12,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libhecate_moe.so")
-SOURCES = ["common.hip", "decode.hip", "router.hip", "prefill.hip", "cputier_gpu.hip", "shared_gemm.hip"]
+SOURCES = ["common.hip", "decode.hip", "router.hip", "norm.hip", "prefill.hip", "cputier_gpu.hip", "shared_gemm.hip"]
 HOST_SOURCES = ["cputier.cpp"]                 # host-only C++ (the CPU expert tier), built with the host compiler
 CXX = os.environ.get("CXX_HOST", "g++")
 # AVX2 / FMA / F16C is the x86-64-v3 level (every AVX2 EPYC and Xeon); no fp contraction, so the q8_0 arithmetic

@@ -1,5 +1,5 @@
 // common.hip - error state of the C ABI, host packers of the gfx950 layouts, device generators of the seeded
-// synthetic layer, dequant, combine, bf16 finish and the residual + RMSNorm kernel.
+// synthetic layer, dequant, combine and bf16 finish (the residual + RMSNorm kernels are in norm.hip).
 #include "hmoe_dev.h"
 #include <cstdarg>
 #include <cstdio>
@@ -154,39 +154,6 @@ __global__ void finish_kernel(float* __restrict__ y, int n, uint16_t* __restrict
     #pragma unroll
     for (int k = 0; k < 4; ++k) out[i + k] = hmoe_f2bf(a[k]);
     *(f32x4*) (y + i) = (f32x4) {0.f, 0.f, 0.f, 0.f};
-}
-
-// residual + RMSNorm, one 256-thread workgroup per row, fixed order (see hecate_moe.h)
-__global__ void __launch_bounds__(256) rmsnorm_kernel(float* __restrict__ r, float* __restrict__ a,
-                                                      const float* __restrict__ w, float eps, uint16_t* __restrict__ xn,
-                                                      _Float16* __restrict__ xh)
-{
-    __shared__ float part[256];
-    const int t = threadIdx.x, row = blockIdx.x;
-    float* v = r + (size_t) row * H;
-    float* av = a ? a + (size_t) row * H : nullptr;
-    float p = 0.f;
-    for (int k = t; k < H; k += 256)
-    {
-        float x = v[k];
-        if (av) { x = x + av[k]; av[k] = 0.f; v[k] = x; }
-        p = __builtin_fmaf(x, x, p);
-    }
-    part[t] = p;
-    __syncthreads();
-    for (int off = 128; off > 0; off >>= 1)
-    {
-        if (t < off) part[t] = part[t] + part[t + off];
-        __syncthreads();
-    }
-    const float mean = part[0] / (float) H;
-    const float rmf = 1.0f / __builtin_sqrtf(mean + eps);
-    for (int k = t; k < H; k += 256)
-    {
-        const uint16_t b = hmoe_f2bf((v[k] * rmf) * w[k]);
-        xn[(size_t) row * H + k] = b;
-        if (xh) xh[(size_t) row * H + k] = (_Float16) bf2f(b);
-    }
 }
 
 static int grid_for(size_t n, int threads, int cap = 65536)
@@ -374,10 +341,3 @@ extern "C" int hmoe_finish_bf16(float* y, int rows, uint16_t* out, void* stream)
     return HMOE_LAUNCHED("finish_bf16");
 }
 
-extern "C" int hmoe_residual_rmsnorm(float* r, float* a, const float* w, int R, float eps, uint16_t* xn, uint16_t* xh,
-                                     void* stream)
-{
-    HMOE_REQUIRE(r && w && xn && R >= 1, "residual_rmsnorm: arguments");
-    rmsnorm_kernel<<<R, 256, 0, (hipStream_t) stream>>>(r, a, w, eps, xn, (_Float16*) xh);
-    return HMOE_LAUNCHED("residual_rmsnorm");
-}

@@ -45,7 +45,6 @@ constexpr int KS_H = H / 32;               // 192 F16T k steps of gate / up
 constexpr int KS_I = I / 32;               // 64 F16T k steps of down
 constexpr int GW = 12;                     // gate/up waves: wave w owns k groups [4w, 4w + 4) of H
 constexpr int DW = 16;                     // down waves: slot w / 4 of the quad, k groups [4 (w % 4), +4) of I
-constexpr int MAX_PARTS = 1 + MAXSLOT / 4;
 constexpr int CTR_WORDS = 1024;            // ctr[0]: the part count of the last down launch
 
 struct __attribute__((aligned(16))) Route
@@ -1005,7 +1004,7 @@ extern "C" size_t hmoe_moe4_scratch_bytes(int which)
 {
     switch (which)
     {
-        case 0: return (size_t) ACT_SLOTS * MAXR * I * 2;               // act f16 [133][16][2048]
+        case 0: return (size_t) ACT_SLOTS * MAXR * I * 2;               // act f16 [134][16][2048]
         case 1: return 256;                                             // gu32 (unused: kept for the argument)
         case 2: return (size_t) CTR_WORDS * 4;                          // ctr_a: the part count
         case 3: return (size_t) MAX_PARTS * MAXR * H * 4;               // y32: down part partials

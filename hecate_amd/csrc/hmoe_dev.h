@@ -21,6 +21,7 @@ constexpr int SH_SLOT = MAXSLOT;            // act slot of the shared expert
 constexpr int SHP_SLOT = MAXSLOT + 1;       // the shared expert's fp32 gate and up sums [2][MAXR][I] (4 slots' room)
 constexpr int REC_SLOT = SHP_SLOT + 4;      // the gate/up launch's routing record for the down launch (int words)
 constexpr int ACT_SLOTS = REC_SLOT + 1;
+constexpr int MAX_PARTS = 1 + MAXSLOT / 4;  // the decode down launch's part partials: the shared expert's, one per slot quad
 constexpr int REC_E = 64;                   // record: word 0 = distinct experts m, words REC_E + j (j < MAXSLOT) = local
                                             // id of slot j (0 past m) | m << 16, so every lane's word carries m
 
@@ -41,6 +42,9 @@ int dense_gate_up(const _Float16* wg, const _Float16* wu, const _Float16* x, int
 enum { DG_MODE_F16 = 0, DG_MODE_ADD = 1 };
 int dense_down(const _Float16* wd, const _Float16* act, int T, void* out, int mode, hipStream_t st);
 int hip_check(hipError_t e, const char* what);
+// the router's select launch for R <= MAXR rows of finished logits [R][RMAXE] (router.hip): one wave per row
+int router_select_small(const float* logits, const float* bias, int R, int E, int topk, float scale, int64_t* sel,
+                        uint16_t* rw, hipStream_t st);
 #define HMOE_REQUIRE(cond, ...) do { if (!(cond)) return ::hmoe::set_error(HMOE_ERR_ARG, __VA_ARGS__); } while (0)
 #define HMOE_LAUNCHED(what) ::hmoe::hip_check(hipGetLastError(), what)
 
@@ -306,10 +310,34 @@ __device__ inline void expert_logits(const uint16_t* __restrict__ x, const float
     }
 }
 
+// ---- RMSNorm in the reduction order of the reference's rms_norm_kernel (runtime/tier/cn.cu:21-31,80-103), which its
+// fused kernels keep bit for bit (nr4_kernel.cuh:4-9): a row of H = 6144 is 1536 float4 columns; chain t (t < 1024)
+// is one fmaf chain from 0 over columns t and t + 1024 (the latter for t < 512), element by element; reduce_1024:
+// an xor butterfly within each group of 32 chains (offsets 16 .. 1), then the same butterfly over the 32 group sums.
+// On gfx950 a group of 32 is a half-wave, so both butterflies run in registers; every lane of a half-wave ends with its
+// group's sum (fp32 addition commutes, so the two partners of each step compute the same value).
+__device__ __forceinline__ float half_wave_sum(float v)
+{
+    #pragma unroll
+    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float chain4(float p, f32x4 v)
+{
+    p = __builtin_fmaf(v[0], v[0], p); p = __builtin_fmaf(v[1], v[1], p);
+    p = __builtin_fmaf(v[2], v[2], p); p = __builtin_fmaf(v[3], v[3], p);
+    return p;
+}
+// rmf = 1 / sqrt(sum / H + eps) * cscale (the reference's rsqrtf, fast math there, as the correctly rounded 1 / sqrt)
+__device__ __forceinline__ float rms_factor(float sum, float eps, float cscale)
+{
+    return (1.0f / __builtin_sqrtf(sum / (float) H + eps)) * cscale;
+}
+
 // The fused input path of the router (nr4_kernel.cuh:122-381: RMSNorm + router in one launch): the residual h fp32
-// [R][H] and the norm weight w; xn = bf16((h * rmf) * w) with rmf = 1 / sqrt(sum_k h^2 / H + eps), the sum in the
-// order of the residual + RMSNorm kernel (256 fmaf chains over k = c, c + 256, ..., folded by halving), so xn is
-// bit-identical to that kernel's. Each workgroup writes its slice of xn (and of xh, the f16 copy, when not NULL).
+// [R][H] and the norm weight w; xn = bf16((h * w) * rmf), rmf from the rms_norm_kernel order above, so xn is
+// bit-identical to the residual + RMSNorm kernel's. Each workgroup writes its slice of xn (and of xh, the f16 copy,
+// when not NULL).
 struct NormIn
 {
     const float* h;
@@ -331,51 +359,66 @@ struct NormIn
 constexpr int LCH = H / RCHUNK;             // 192 chunks
 constexpr int WST = RCHUNK + 4;             // weight chunk stride, floats
 constexpr int XST = RCHUNK / 2 + 4;         // x chunk stride, u32 words (two bf16 each)
-template <bool NORM, int EPW = 2>
+// XF16: x holds f16 values (bf16 otherwise); WF16: the weight rows are f16 (fp32 otherwise), widened exactly when staged.
+template <bool XF16> __device__ __forceinline__ float x_lo(uint32_t v)
+{
+    return XF16 ? (float) __builtin_bit_cast(_Float16, (uint16_t) (v & 0xffffu)) : __uint_as_float(v << 16);
+}
+template <bool XF16> __device__ __forceinline__ float x_hi(uint32_t v)
+{
+    return XF16 ? (float) __builtin_bit_cast(_Float16, (uint16_t) (v >> 16)) : __uint_as_float(v & 0xffff0000u);
+}
+
+template <bool NORM, int EPW = 2, bool XF16 = false, bool WF16 = false>
 __device__ inline void pair_logits(const uint16_t* __restrict__ x, const NormIn& nin, const float* __restrict__ wt,
                                    int e0, int E, int R, float* __restrict__ logits)
 {
     static_assert(EPW == 1 || EPW == 2, "one or two experts per workgroup");
     static_assert(!NORM || EPW == 2, "the RMSNorm input path splits rows over two halves of 256 threads");
+    static_assert(!(NORM && XF16), "the RMSNorm input path forms bf16 rows");
     constexpr int NTH = 256 * EPW, XP = 3072 / NTH;             // threads; x pieces per thread and group of 4 rows
     __shared__ __attribute__((aligned(16))) float ws[EPW][LCH * WST];
     __shared__ __attribute__((aligned(16))) uint32_t xs[4][LCH * XST];
     __shared__ __attribute__((aligned(16))) float sums[EPW][LCH][MAXR + 1];
     __shared__ float segs[EPW][MAXR][RSEG];
     __shared__ float rmfs[MAXR];
+    __shared__ float gsum[MAXR][32];
     const int t = threadIdx.x, half = t >> 8, c = t & 255;
     // the weight rows: EPW x 1536 pieces of 4 floats, 6 per thread (a row past E re-reads row E - 1)
     #pragma unroll
     for (int i = 0; i < 6; ++i)
     {
         const int p = t + NTH * i, h = p / 1536, q = p - h * 1536;
-        const f32x4 v = *(const f32x4*) (wt + (size_t) min(e0 + h, E - 1) * H + 4 * q);
+        const size_t wo = (size_t) min(e0 + h, E - 1) * H + 4 * q;
+        f32x4 v;
+        if (WF16)
+        {
+            const u32x2 u = *(const u32x2*) ((const uint16_t*) wt + wo);
+            v = (f32x4) {x_lo<true>(u[0]), x_hi<true>(u[0]), x_lo<true>(u[1]), x_hi<true>(u[1])};
+        }
+        else v = *(const f32x4*) (wt + wo);
         *(f32x4*) &ws[h][(q >> 3) * WST + 4 * (q & 7)] = v;
     }
-    if (NORM)
+    if constexpr (NORM)
     {
-        // rmf of every row: chain c of row r by thread (r % 2) * 256 + c, the halving fold in sums (as [R][256])
-        float (*part)[256] = reinterpret_cast<float (*)[256]>(&sums[0][0][0]);
-        for (int r = half; r < R; r += 2)
+        // rmf of every row in the rms_norm_kernel order: thread t (of 512) runs chains t (columns t and t + 1024) and
+        // t + 512 (column t + 512); half-wave g sums groups g and g + 16 in registers, the 32 group sums of a row go
+        // to gsum, and half-wave r < R sums row r's
+        static_assert(NTH == 512, "the norm's chains are laid out for 512 threads");
+        for (int r = 0; r < R; ++r)
         {
-            const float* v = nin.h + (size_t) r * H + c;
-            float hv[H / 256];
-            #pragma unroll
-            for (int j = 0; j < H / 256; ++j) hv[j] = v[256 * j];
-            float p = 0.f;
-            #pragma unroll
-            for (int j = 0; j < H / 256; ++j) p = __builtin_fmaf(hv[j], hv[j], p);
-            part[r][c] = p;
+            const f32x4* v = (const f32x4*) (nin.h + (size_t) r * H);
+            const f32x4 a = v[t], b2 = v[t + 1024], m = v[t + 512];
+            const float c0 = half_wave_sum(chain4(chain4(0.f, a), b2)), c1 = half_wave_sum(chain4(0.f, m));
+            if ((t & 31) == 0) { gsum[r][t >> 5] = c0; gsum[r][16 + (t >> 5)] = c1; }
         }
         __syncthreads();
-        for (int off = 128; off > 0; off >>= 1)
+        if ((t >> 5) < R)
         {
-            for (int r = half; r < R; r += 2)
-                if (c < off) part[r][c] = part[r][c] + part[r][c + off];
-            __syncthreads();
+            const float tot = half_wave_sum(gsum[t >> 5][t & 31]);
+            if ((t & 31) == 0) rmfs[t >> 5] = rms_factor(tot, nin.eps, 1.0f);
         }
-        if (t < R) rmfs[t] = 1.0f / __builtin_sqrtf(part[t][0] / (float) H + nin.eps);
-        __syncthreads();                                        // (sums is written again by the chains below)
+        __syncthreads();
     }
     // rows r0 .. r0 + 3 of x: 4 x 768 pieces of 8 bf16, XP per thread (rows past R re-read row R - 1); the next
     // group's loads are in flight while the current group computes (NORM: formed at the start of each group, and
@@ -412,7 +455,7 @@ __device__ inline void pair_logits(const uint16_t* __restrict__ x, const NormIn&
             {
                 const float a0 = e < 2 ? h0[2 * e] : h1[2 * e - 4], a1 = e < 2 ? h0[2 * e + 1] : h1[2 * e - 3];
                 const float b0 = e < 2 ? w0[2 * e] : w1[2 * e - 4], b1 = e < 2 ? w0[2 * e + 1] : w1[2 * e - 3];
-                v[e] = (uint32_t) hmoe_f2bf((a0 * rf) * b0) | ((uint32_t) hmoe_f2bf((a1 * rf) * b1) << 16);
+                v[e] = (uint32_t) hmoe_f2bf((a0 * b0) * rf) | ((uint32_t) hmoe_f2bf((a1 * b1) * rf) << 16);
             }
             *(u32x4*) &xs[j][(q >> 2) * XST + 4 * (q & 3)] = v;
             if (r0 + j < R && (int) ((q * ((E + EPW - 1) / EPW)) / 768) == (int) blockIdx.x)
@@ -467,8 +510,8 @@ __device__ inline void pair_logits(const uint16_t* __restrict__ x, const NormIn&
                     #pragma unroll
                     for (int k = 0; k < 4; ++k)
                     {
-                        acc = __builtin_fmaf(__uint_as_float(xv[i][k] << 16), wv[8 * i + 2 * k], acc);
-                        acc = __builtin_fmaf(__uint_as_float(xv[i][k] & 0xffff0000u), wv[8 * i + 2 * k + 1], acc);
+                        acc = __builtin_fmaf(x_lo<XF16>(xv[i][k]), wv[8 * i + 2 * k], acc);
+                        acc = __builtin_fmaf(x_hi<XF16>(xv[i][k]), wv[8 * i + 2 * k + 1], acc);
                     }
                 sums[half][c][r0 + j] = acc;
             }

@@ -178,6 +178,13 @@ __global__ void __launch_bounds__(256) router_select_kernel(const float* __restr
         }
 }
 
+int router_select_small(const float* logits, const float* bias, int R, int E, int topk, float scale, int64_t* sel,
+                        uint16_t* rw, hipStream_t st)
+{
+    router_select_small_kernel<<<1, 1024, 0, st>>>(logits, bias, R, E, topk, scale, sel, rw);
+    return HMOE_LAUNCHED("router select");
+}
+
 }  // namespace hmoe
 
 using namespace hmoe;
@@ -207,8 +214,8 @@ extern "C" int hmoe_router_fused(const void* x, const float* wt, const float* bi
             router_logits_h_kernel<<<(E + 1) / 2, 512, 0, st>>>((const uint16_t*) x, wt, logits, R, E, (_Float16*) xh);
         else
             router_logits_kernel<<<(E + 1) / 2, 512, 0, st>>>((const uint16_t*) x, wt, logits, R, K, E, (_Float16*) xh);
-        router_select_small_kernel<<<1, 1024, 0, st>>>(logits, bias, R, E, topk, scale, sel, rw);
-        return HMOE_LAUNCHED("router_fused");
+        if (int rc = HMOE_LAUNCHED("router_fused")) return rc;
+        return router_select_small(logits, bias, R, E, topk, scale, sel, rw, st);
     }
     // 128 experts per workgroup from 4096 rows (the 8 x 8 tiles are faster at 8192 rows, -115 us); fewer rows take 64
     // experts per workgroup, so that the grid still fills the CUs twice over

@@ -38,7 +38,10 @@ def forward(x, tok, eid, wt, rbt, gw, uw, dw, gs, us, ds, gu, ar, d, out, meta=N
     npos = tok.numel() if npos is None else int(npos)
     nrb = rbt.shape[0] if nrb is None else int(nrb)
     ps = ar.shape[0]
-    if npos > ps or ar.shape[1] != I or ar.dtype != torch.float16 or d.numel() < ps * H or d.dtype != torch.float32:
+    # d: the reference's fp32 [1, ps, H] (moe4t.scratch) or an f16 [ps, H] buffer: the kernels write f16 rows into it
+    # (the copy of bf16 x, then with inv each pick's down row), ps * H * 2 bytes
+    if npos > ps or ar.shape[1] != I or ar.dtype != torch.float16 or d.dtype not in (torch.float32, torch.float16) \
+            or d.numel() * d.element_size() < ps * H * 2 or not d.is_contiguous():
         raise RuntimeError(f"moe4t: scratch for {ps} picks, {npos} given")
     if out_bf16 is not None:
         if inv is None or out_bf16.dtype != torch.bfloat16 or not out_bf16.is_contiguous() \

@@ -5,7 +5,7 @@ router_fused(x, wt, bias, logits, ctr, sel, rw, topk, scale) keeps the reference
 """
 import torch
 
-from ._lib import call, lib, on_device, ptr, stream_of
+from ._lib import call, dt_of, lib, on_device, ptr, stream_of
 
 
 def buffers(R, device, E=256):
@@ -43,3 +43,31 @@ def norm_router(h, norm_w, eps, wt, logits, xn, xh=None):
     call("hmoe_norm_router", ptr(h), ptr(norm_w), float(eps), int(R), ptr(wt), int(E), ptr(logits), ptr(xn), ptr(xh),
          stream_of(h.device))
     return xn
+
+
+def norm_route_buffers(R, device, E=256):
+    """(cand, ctr) scratch of norm_route for up to R rows: the logits buffer and the reference's counter argument"""
+    dev = torch.device(device)
+    n = int(lib().hmoe_norm_route_scratch_bytes(R, E)) // 4
+    return torch.zeros(n, dtype=torch.float32, device=dev), torch.zeros(64, dtype=torch.int32, device=dev)
+
+
+def norm_route(y, r, w, x2, gt, bias, sel, rw, cand, ctr, scale, eps, cbias=0.0, cscale=1.0, ho=None):
+    """runtime/core/exl3_normroute.py:16-65 norm_route (nr4_kernel.cuh:122-381): r = y + r, x2 = RMSNorm(r) * (w +
+    cbias) * cscale (fp16 as in the reference, or bf16), then the router on x2: gt [E, H] fp16 (the reference's
+    transposed gate) or fp32, bias fp32 [E] or None, sel int64 / rw fp16 [R, 8]. cand / ctr: norm_route_buffers. ho
+    (the reference's band hand-off words) must be empty: post the CPU tier's job with CpuTier after the routing."""
+    on_device("norm_route", y, r, w, x2, gt, bias, sel, rw, cand, ctr)
+    R = y.numel() // y.shape[-1]
+    E = gt.shape[0]
+    if ho:
+        raise RuntimeError("norm_route: the band hand-off (ho) is not supported; post the CPU tier's job after routing")
+    if not (y.dtype == torch.float32 and r.dtype == torch.float32 and y.shape[-1] == 6144 and r.numel() == y.numel()
+            and x2.numel() >= y.numel() and y.is_contiguous() and r.is_contiguous() and x2.is_contiguous()
+            and gt.is_contiguous() and gt.shape[1] == 6144 and w.numel() == 6144 and sel.dtype == torch.int64
+            and rw.dtype == torch.float16 and cand.numel() * 4 >= int(lib().hmoe_norm_route_scratch_bytes(R, E))):
+        raise RuntimeError("norm_route: shape / dtype")
+    call("hmoe_norm_route", ptr(y), ptr(r), ptr(w), ptr(x2), ptr(gt), ptr(bias), ptr(sel), ptr(rw), ptr(cand),
+         ptr(ctr), float(scale), float(eps), float(cbias), float(cscale), None, 0, int(R), int(E), dt_of(w),
+         dt_of(x2, ("bfloat16", "float16")), dt_of(gt, ("float32", "float16")), stream_of(y.device))
+    return sel, rw

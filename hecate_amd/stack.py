@@ -1,17 +1,21 @@
 """A decode step through consecutive MoE layers with the residual + RMSNorm between them, as one hipGraph.
 
-h = x (fp32); per layer l: xn = bf16(RMSNorm(h) w_l), route(xn), h += routed + shared experts of xn.
+h = x (fp32); per layer l: xn = bf16(RMSNorm(h) w_l), route(xn), h += routed + shared experts of xn. Every norm uses
+the reduction order of the reference's rms_norm_kernel (include/hecate_moe.h).
 
-fused (default): four launches per layer: RMSNorm + router logits (runtime/tier/nr4_kernel.cuh:122-381), then the
-decode layer's gate/up, down and output launches, the last adding the layer's output into h (the combine of
-runtime/tier/cn.cu:48-103). Unfused: five launches per layer, the combine folded into the next layer's input norm
-(cn.cu:48-103: r += y_(l-1), y zeroed, then the norm), the router in the decode layer, and one final combine; both
-give the same bits. Static-shaped and allocation-free either way.
+fused (default), by row count:
+  one row   three launches per layer: RMSNorm + router logits (runtime/tier/nr4_kernel.cuh:122-381), then the
+            decode layer's gate/up and down launches, the down launch adding the layer's output into h itself;
+  more rows four launches per layer: the router logits of xn, gate/up, the down partials, then the layer's output
+            combine fused with the next layer's input norm (runtime/tier/cn.cu:48-103, hmoe_decode_combine_norm: the
+            parts summed in order, h += them, xn of the next layer); after the last layer the plain output launch.
+Unfused: the residual + RMSNorm kernel, the router inside the decode layer, the output into y, and one final combine.
+All forms give the same bits. Static-shaped and allocation-free either way.
 """
 import torch
 
 from . import moe4, router
-from ._lib import call, ptr, stream_of
+from ._lib import DT_BF16, DT_F32, call, ptr, stream_of
 
 H = 6144
 
@@ -33,19 +37,34 @@ class DecodeStack:
 
     def step(self, trace=None, fused=True):
         """one step; trace (eager only): a list that receives per layer (residual at the layer's input, xn, y, sel,
-        rw); fused: y is added into the residual by the layer's output launch, and its trace entry is None"""
+        rw); in the fused forms the layer output is never materialised and its trace entry is None"""
         R = self.R
         self.h.copy_(self.x)
         st = stream_of(self.h.device)
+        L = len(self.layers)
+        parts = fused and R > 1
+        if parts:
+            call("hmoe_residual_rmsnorm", ptr(self.h), None, ptr(self.norm_w[0]), R, float(self.eps), ptr(self.xn),
+                 None, st)
         for l, lay in enumerate(self.layers):
-            if fused:
+            if fused and not parts:
                 router.norm_router(self.h, self.norm_w[l], self.eps, lay.wg, lay.logits, self.xn)
-            else:
+            elif not fused:
                 call("hmoe_residual_rmsnorm", ptr(self.h), ptr(self.y) if l > 0 else None, ptr(self.norm_w[l]), R,
                      float(self.eps), ptr(self.xn), None, st)
             if trace is not None:
                 trace.append([self.h.clone(), self.xn.clone()])
-            if fused:
+            if parts:
+                # router logits, gate/up, down partials; then the parts into h with the next layer's norm (or, after
+                # the last layer, the plain output launch adding them into h)
+                lay.decode(self.xn, y=self.h, out=False, phases=7)
+                if l + 1 < L:
+                    act, gu32, ctr_a, y32, _ = lay.scr
+                    call("hmoe_decode_combine_norm", ptr(y32), ptr(ctr_a), R, ptr(self.h), ptr(self.norm_w[l + 1]),
+                         ptr(self.xn), None, float(self.eps), 0.0, 1.0, DT_F32, DT_BF16, st)
+                else:
+                    lay.decode(self.xn, y=self.h, out=False, phases=8)
+            elif fused:
                 lay.decode(self.xn, y=self.h, out=False, phases=14)
             else:
                 lay.decode(self.xn, y=self.y, out=False)

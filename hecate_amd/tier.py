@@ -228,9 +228,10 @@ class PrefillBuffers:
         self.rbt, self.meta = z(self.nrb_max, 4), z(4)
         self.work = z(int(L.hmoe_dispatch_work_bytes(T, topk, n)) // 4 + 1)
         if long:
-            # moe4t's ar and d (its gu is unused: not allocated) and the shared expert's work
+            # moe4t's ar and d (its gu is unused: not allocated; d as the f16 rows the kernels write, half the
+            # reference's fp32 buffer) and the shared expert's work
             self.scr = [None, torch.empty((F, I), dtype=torch.float16, device=dev),
-                        torch.empty((1, F, H), dtype=torch.float32, device=dev)]
+                        torch.empty((F, H), dtype=torch.float16, device=dev)]
             self.shw = torch.empty(int(L.hmoe_shared_work_bytes(T)) // 4 + 64, dtype=torch.float32, device=dev)
         else:
             self.scr = moe4p.scratch(dev, F, T)
@@ -332,10 +333,11 @@ class MoELayer:
         return self._pf
 
     def prefill_experts(self, x, y, with_shared=True, out_bf16=None):
-        """routed (+ shared) experts of x's routed selection (in the prefill buffers) added into y fp32 [T, H]; with
-        out_bf16 (bf16 [T, H]) the layer output bf16(y + experts) is written there instead and y left zeroed (moe4p:
-        y, kept zeroed, is not touched; moe4t with the ordered combine: y is rounded and re-zeroed by the combine);
-        returns whether it was"""
+        """routed (+ shared) experts of x's routed selection (in the prefill buffers) added into y fp32 [T, H].
+        With out_bf16 (bf16 [T, H]) the layer output bf16(experts) is written there instead, and y must hold zeros on
+        entry (as MoELayer keeps it) and holds zeros on return: the moe4p form never reads y, the moe4t form (ordered
+        combine) adds the shared expert into y first and its combine rounds y + picks and re-zeroes y. Returns whether
+        out_bf16 was written (the atomic moe4t form adds into y instead)."""
         T = x.shape[0]
         pf = self._pf
         gq, uq, dq, gs, us, ds = self.bank.tables()
@@ -370,7 +372,9 @@ class MoELayer:
     def prefill(self, x, with_shared=True):
         """the prefill layer: bf16 [T, H] out (router, device dispatch plan, grouped GEMMs, per-token combine); an
         empty chunk gives an empty output (tier_split.py:377 returns out when no pick reaches the tier). Chunks of more
-        than LONG_ROWS rows run the routed experts on moe4t (256-pick blocks, atomic combine), as the reference does"""
+        than LONG_ROWS rows run the routed experts on moe4t (256-pick blocks), as the reference does, with the ordered
+        per-token combine through the inverse map (deterministic; MoELayer.deterministic = False takes the reference's
+        atomic down epilogue)"""
         T = x.shape[0]
         on_device("prefill", x, self.wg)
         if T == 0:

@@ -202,7 +202,8 @@ int hmoe_moe4p_forward_bf16(const void* x, const int* tok, const int* eid, const
  * topk): the down rows go to d and each token adds its picks in top-k order (deterministic, and cheaper on gfx950
  * than scattered fp32 atomics). Scratch
  * (hmoe_moe4t_scratch_bytes(which, npos)): gu fp32 [2][npos][I] (unused, kept for the argument), ar f16 [npos][I],
- * d fp32 [1][npos][H] (holds the f16 copy of x when x is bf16; the reference gathers the picks' rows into it).
+ * d fp32 [1][npos][H] (the reference's size; the kernels write f16 rows into it, the copy of x when x is bf16 and with
+ * inv each pick's down row, so npos * H * 2 bytes suffice; the reference gathers the picks' rows into it).
  * T: rows of x and out; meta as in moe4p (the device plan's {npos, nrb}, or NULL); no shared expert (the reference
  * runs it apart at prefill: hmoe_shared_forward). npos = 0 is a no-op (moe4t.cu:508). */
 size_t hmoe_moe4t_scratch_bytes(int which, int npos);      /* which: 0 gu, 1 ar, 2 d */
@@ -236,18 +237,53 @@ size_t hmoe_shared_work_bytes(int T);
 int hmoe_shared_forward(const void* x, int T, const void* sh_gw, const void* sh_uw, const void* sh_dw, void* work,
                         float* out, int xf, void* stream);
 
-/* ---- residual + RMSNorm between layers: runtime/tier/cn.cu:48-103 (combine_norm) restated for fp32 weights ----
- * r fp32 [R][H] residual += a (a fp32 [R][H] or NULL; a is zeroed after use), xn = bf16(r * rsqrt(mean r^2 + eps) * w)
- * in one fixed fp32 order: 256 fmaf chains over k = t, t + 256, ..., folded by halving (t += t + off, off = 128..1),
- * rmf = 1 / sqrt(sum / H + eps), xn = bf16((r * rmf) * w); xh optional f16 copy of xn. */
+/* ---- residual + RMSNorm: runtime/tier/cn.cu and runtime/core/nr4_kernel.cuh ----
+ * Every RMSNorm here uses the reduction order of the reference's rms_norm_kernel, which its fused kernels reproduce
+ * bit for bit (cn.cu:1-6,21-31,80-103; nr4_kernel.cuh:4-9): a row is H / 4 = 1536 float4 columns, chain t of 1024
+ * is one fmaf chain from 0 over the elements of columns t and t + 1024 (t < 512), the chains of each group of 32 are
+ * summed by an xor butterfly (offsets 16, 8, 4, 2, 1), the 32 group sums by the same butterfly;
+ * rmf = 1 / sqrt(sum / H + eps) * cscale (the reference's rsqrtf, fast math there, as the correctly rounded 1 / sqrt
+ * here), xn = (r * (w + cbias)) * rmf with cbias added only when nonzero, rounded to the output type. w: fp32, bf16 or
+ * f16 [H] (w_dtype); xn: bf16 or f16 [rows][H] (xn_dtype). Rows are 16-byte aligned fp32, xn 8-byte aligned. */
+enum { HMOE_DT_F32 = 0, HMOE_DT_BF16 = 1, HMOE_DT_F16 = 2 };
+/* runtime/tier/cn.cu:189-235 combine_norm(f, o_ptr, y, rows, o2_ptr, done_ptr, r, w, xn, eps, cbias, cscale): the MoE
+ * combine of a layer fused into the next input norm, one workgroup per row: a = ((f + y) + o) + o2 (f may be NULL, read
+ * as +0 as combine_norm_pdl does, cn.cu:105-110; o, o2 may be NULL), y zeroed, r = a + r, xn = RMSNorm(r). f, y, o, o2,
+ * r fp32 [rows][H]; rows in [1, 64]. done must be NULL (the RTX band's DONE flag: that band is not built). */
+int hmoe_combine_norm(const float* f, const float* o, float* y, int rows, const float* o2, const unsigned* done,
+                      float* r, const void* w, void* xn, float eps, float cbias, float cscale, int w_dtype,
+                      int xn_dtype, void* stream);
+/* runtime/core/exl3_normroute.py:16-65 norm_route(y, r, w, x2, gt, bias, sel, rw, cand, ctr, scale, eps, cbias, cscale,
+ * ho) (nr4_kernel.cuh:122-381): the post-attention residual add and RMSNorm, then the router on the normed rows:
+ * r = y + r (y fp32 [R][H], read only), x2 = RMSNorm(r) (bf16 or f16, x2_dtype), logits of x2 against gt ([E][H],
+ * fp32 or the reference's f16, gt_dtype) in router_fused's fixed order, sel int64 / rw f16 [R][8] by router_fused's
+ * rules (sigmoid + bias keys, ties to the lowest index, rw = f16(a * scale / (sum a + 1e-20))). cand: logits scratch of
+ * hmoe_norm_route_scratch_bytes(R, E) bytes (the reference's candidate buffer has the same role); ctr unused (kept for
+ * the argument position). ho: the reference's band hand-off words; n_ho must be 0 (the CPU tier's job is posted by
+ * hmoe_cpu_submit after the routing). R in [1, 16] (the reference: 2..8), E in [8, 256]. Three launches: the norm
+ * (one workgroup per row), the logits (two experts per workgroup), the selection; r and x2 are those of
+ * hmoe_combine_norm's norm, the routing that of hmoe_router_fused on x2. */
+size_t hmoe_norm_route_scratch_bytes(int R, int E);
+int hmoe_norm_route(const float* y, float* r, const void* w, void* x2, const void* gt, const float* bias, int64_t* sel,
+                    uint16_t* rw, float* cand, int* ctr, float scale, float eps, float cbias, float cscale,
+                    const int64_t* ho, int n_ho, int R, int E, int w_dtype, int x2_dtype, int gt_dtype, void* stream);
+/* the decode layer's output launch fused with the next layer's input norm (this build's addition: cn.cu:48-103's
+ * combine-into-norm for the part-sum decode form): s = the down launch's part partials (y32, their count in ctr_a, as
+ * hmoe_moe_decode_layer left them with phases 2 | 4 at R > 1, or with bit 16 at any R) summed in part order, r = s + r
+ * (the bits of that layer's output launch adding into r), xn = RMSNorm(r) as above, xh optional f16 copy of xn. R in
+ * [1, 16]. */
+int hmoe_decode_combine_norm(const float* y32, const int* ctr_a, int R, float* r, const void* w, void* xn, void* xh,
+                             float eps, float cbias, float cscale, int w_dtype, int xn_dtype, void* stream);
+/* residual + RMSNorm between layers (cn.cu:80-103 with the layer output as a): r = a + r (a fp32 [R][H] or NULL; a is
+ * zeroed after use), xn = bf16 RMSNorm(r) with fp32 w, cbias 0, cscale 1; xh optional f16 copy of xn. */
 int hmoe_residual_rmsnorm(float* r, float* a, const float* w, int R, float eps, uint16_t* xn, uint16_t* xh,
                           void* stream);
-/* ---- RMSNorm + router in one launch: runtime/tier/nr4_kernel.cuh:122-381 (nr4_kernel: norm, router scores) ----
- * h fp32 [R][H] (the residual, read only; R <= 16), norm_w fp32 [H]: xn = bf16(h * rsqrt(mean h^2 + eps) * norm_w) in
- * the order of hmoe_residual_rmsnorm (bit-identical to it with a = NULL), xh optional f16 copy of xn, and the router
- * logits of xn into logits, as phase 1 of hmoe_moe_decode_layer computes them; run hmoe_moe_decode_layer on xn with
- * the same logits and phases 14 to finish the layer. Passing y = h to that call adds the layer's output into the
- * residual (the combine of runtime/tier/cn.cu:48-103), so a decode stack needs one norm + router launch per layer. */
+/* ---- RMSNorm + router logits in one launch: runtime/tier/nr4_kernel.cuh:122-381 (nr4_kernel: norm, router scores) --
+ * h fp32 [R][H] (the residual, read only; R <= 16), norm_w fp32 [H]: xn = bf16 RMSNorm(h) (bit-identical to
+ * hmoe_residual_rmsnorm with a = NULL), xh optional f16 copy of xn, and the router logits of xn into logits, as phase 1
+ * of hmoe_moe_decode_layer computes them; run hmoe_moe_decode_layer on xn with the same logits and phases 14 to finish
+ * the layer. Passing y = h to that call adds the layer's output into the residual (the combine of cn.cu:48-103), so a
+ * decode stack at one row needs three launches per layer. */
 int hmoe_norm_router(const float* h, const float* norm_w, float eps, int R, const float* wt, int E, float* logits,
                      uint16_t* xn, void* xh, void* stream);
 

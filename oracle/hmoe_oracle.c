@@ -63,13 +63,13 @@ float orc_expf(float x) { return hmoe_expf(x); }
  * (k ascending, from 0) whose totals are added in order from 0; the segment totals added in order from 0
  * (K % 256 == 0). The reference accumulates the same products in fp32 with atomics (exl3_router.py:42-71: fp32
  * accumulation of fp16 products, order set by the atomics); here W_g is fp32. */
-void orc_router_logits(const uint16_t* x, const float* w, int R, int K, int E, float* logits)
+void orc_router_logits_f32(const float* x, const float* w, int R, int K, int E, float* logits)
 {
     #pragma omp parallel for collapse(2) schedule(static)
     for (int r = 0; r < R; ++r)
         for (int e = 0; e < E; ++e)
         {
-            const uint16_t* xr = x + (size_t) r * K;
+            const float* xr = x + (size_t) r * K;
             const float* we = w + (size_t) e * K;
             const int SEG = K / ORC_ROUTER_SEGMENTS;
             float t = 0.0f;
@@ -79,13 +79,22 @@ void orc_router_logits(const uint16_t* x, const float* w, int R, int K, int E, f
                 for (int c = s0; c < s0 + SEG; c += ORC_ROUTER_CHUNK)
                 {
                     float acc = 0.0f;
-                    for (int k = c; k < c + ORC_ROUTER_CHUNK; ++k) acc = fmaf(hmoe_bf2f(xr[k]), we[k], acc);
+                    for (int k = c; k < c + ORC_ROUTER_CHUNK; ++k) acc = fmaf(xr[k], we[k], acc);
                     seg = seg + acc;
                 }
                 t = t + seg;
             }
             logits[(size_t) r * E + e] = t;
         }
+}
+
+/* x bf16: widened exactly, then the fp32 form */
+void orc_router_logits(const uint16_t* x, const float* w, int R, int K, int E, float* logits)
+{
+    float* xf = (float*) malloc((size_t) R * K * sizeof(float));
+    for (size_t i = 0; i < (size_t) R * K; ++i) xf[i] = hmoe_bf2f(x[i]);
+    orc_router_logits_f32(xf, w, R, K, E, logits);
+    free(xf);
 }
 
 /* exl3_router.py:84-128: a = sigmoid(l); key = okey(a + bias); topk rounds of (max key, lowest index on ties), so
@@ -465,21 +474,63 @@ int orc_moe(int mode, int R, int H, int I, const uint16_t* x, const int64_t* sel
 }
 
 /* ------------------------------------------------------------------------------------------------------------------
- * residual + RMSNorm (cn.cu:80-103: r += a, xn = r * rsqrt(mean r^2 + eps) * w), in this build's fixed fp32 order:
- * 256 fmaf chains (chain t over k = t, t + 256, ...), folded by halving (t += t + off, off = 128 .. 1),
- * rmf = 1 / sqrt(sum / H + eps), xn = bf16((r * rmf) * w). a may be NULL.
+ * RMSNorm in the reduction order of the reference's rms_norm_kernel, which its fused kernels reproduce bit for bit
+ * (combine_norm, runtime/tier/cn.cu:1-6,21-31,80-103; norm_route, runtime/core/nr4_kernel.cuh:4-9,176-243):
+ * a row of H values is H / 4 float4 columns; thread t of 1024 owns columns t, t + 1024, ... (< H / 4) and runs one
+ * fmaf chain from 0 over its columns' elements in order (cn.cu:80-87); reduce_1024 (cn.cu:21-31): within each group
+ * of 32 threads an xor butterfly (offsets 16, 8, 4, 2, 1; every lane ends with the group's sum), then the 32 group
+ * sums, in group order, by the same butterfly. rmf = 1 / sqrt(sum / H + eps) * cscale (cn.cu:89: rsqrtf under
+ * fast math there, the correctly rounded 1 / sqrt here), xn = (v * (w + cbias)) * rmf (cbias added only when nonzero,
+ * cn.cu:95-96), rounded to bf16 (xn_bf16 = 1) or f16 (0). v: the residual after the add, [R][H].
  * ---------------------------------------------------------------------------------------------------------------- */
-void orc_residual_rmsnorm(float* r, const float* a, const float* w, int R, int H, float eps, uint16_t* xn_bf16)
+static float butterfly32(const float* in)
+{
+    float l[32], n[32];
+    memcpy(l, in, sizeof(l));
+    for (int o = 16; o > 0; o >>= 1)
+    {
+        for (int i = 0; i < 32; ++i) n[i] = l[i] + l[i ^ o];
+        memcpy(l, n, sizeof(l));
+    }
+    return l[0];
+}
+
+float orc_rms_sum(const float* v, int H)
+{
+    const int C = H / 4;
+    float chain[1024], gs[32];
+    for (int t = 0; t < 1024; ++t)
+    {
+        float p = 0.0f;
+        for (int c = t; c < C; c += 1024)
+            for (int e = 0; e < 4; ++e) p = fmaf(v[4 * c + e], v[4 * c + e], p);
+        chain[t] = p;
+    }
+    for (int g = 0; g < 32; ++g) gs[g] = butterfly32(chain + 32 * g);
+    return butterfly32(gs);
+}
+
+void orc_rmsnorm_cn(const float* v, const float* w, int R, int H, float eps, float cbias, float cscale, int xn_bf16,
+                    uint16_t* xn)
 {
     for (int row = 0; row < R; ++row)
     {
-        float* v = r + (size_t) row * H;
-        if (a) for (int k = 0; k < H; ++k) v[k] = v[k] + a[(size_t) row * H + k];
-        float part[256];
-        for (int t = 0; t < 256; ++t) { float p = 0.0f; for (int k = t; k < H; k += 256) p = fmaf(v[k], v[k], p); part[t] = p; }
-        for (int off = 128; off > 0; off >>= 1) for (int t = 0; t < off; ++t) part[t] = part[t] + part[t + off];
-        const float mean = part[0] / (float) H;
-        const float rmf = 1.0f / sqrtf(mean + eps);
-        for (int k = 0; k < H; ++k) xn_bf16[(size_t) row * H + k] = hmoe_f2bf((v[k] * rmf) * w[k]);
+        const float* vr = v + (size_t) row * H;
+        const float rmf = (1.0f / sqrtf(orc_rms_sum(vr, H) / (float) H + eps)) * cscale;
+        for (int k = 0; k < H; ++k)
+        {
+            const float wk = cbias != 0.0f ? w[k] + cbias : w[k];
+            const float o = (vr[k] * wk) * rmf;
+            xn[(size_t) row * H + k] = xn_bf16 ? hmoe_f2bf(o) : hmoe_f2h(o);
+        }
     }
+}
+
+/* residual + RMSNorm between layers (cn.cu:80-103 with f = y = 0 and a the layer output): r = a + r (a may be NULL),
+ * then orc_rmsnorm_cn with cbias 0, cscale 1, bf16 out */
+void orc_residual_rmsnorm(float* r, const float* a, const float* w, int R, int H, float eps, uint16_t* xn_bf16)
+{
+    if (a)
+        for (size_t i = 0; i < (size_t) R * H; ++i) r[i] = a[i] + r[i];
+    orc_rmsnorm_cn(r, w, R, H, eps, 0.0f, 1.0f, 1, xn_bf16);
 }

@@ -37,6 +37,8 @@ void orc_f16_to_f32(const uint16_t* in, int64_t n, float* out);
 float orc_expf(float x);
 
 /* ---- router: exl3_router.py:86-131, nr4_kernel.cuh:307-366 ---- */
+/* the same order on fp32 rows (x widened exactly from bf16 or f16 by the caller) */
+void orc_router_logits_f32(const float* x, const float* w, int R, int K, int E, float* logits);
 void orc_router_logits(const uint16_t* x, const float* w, int R, int K, int E, float* logits);
 void orc_router_select(const float* logits, const float* bias, int R, int E, int topk, float scale,
                        int64_t* sel, uint16_t* rw);
@@ -61,7 +63,11 @@ int orc_picks(const int64_t* sel, const uint16_t* rw, int R, int topk, int lo, i
 /* ---- dequant (moe4.cu:679-698 restated for g128): codes + scales -> fp32 [N][K] ---- */
 void orc_dequant(const uint8_t* codes, const uint16_t* scales, int N, int K, float* out);
 
-/* ---- RMSNorm with residual: cn.cu:48-103 restated in fp32 (fixed order) ---- */
+/* ---- RMSNorm in the reference's rms_norm_kernel order (cn.cu:21-31,80-103; nr4_kernel.cuh:176-243) ---- */
+float orc_rms_sum(const float* v, int H);
+void orc_rmsnorm_cn(const float* v, const float* w, int R, int H, float eps, float cbias, float cscale, int xn_bf16,
+                    uint16_t* xn);
+/* r = a + r (a may be NULL), then orc_rmsnorm_cn (cbias 0, cscale 1, bf16 out) */
 void orc_residual_rmsnorm(float* r, const float* a, const float* w, int R, int H, float eps, uint16_t* xn_bf16);
 
 #ifdef __cplusplus

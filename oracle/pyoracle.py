@@ -37,6 +37,7 @@ def lib():
             "orc_f16_to_f32": (None, [P, i64, P]),
             "orc_expf": (f32, [f32]),
             "orc_router_logits": (None, [P, P, i32, i32, i32, P]),
+            "orc_router_logits_f32": (None, [P, P, i32, i32, i32, P]),
             "orc_router_select": (None, [P, P, i32, i32, i32, f32, P, P]),
             "orc_dispatch": (i32, [P, P, i32, i32, i32, i32, P, P, P, P, P]),
             "orc_pick_groups": (i32, [P, i32, i32, i32, P, i32]),
@@ -45,6 +46,8 @@ def lib():
             "orc_q8_gemv": (i32, [P, P, i32, i32, P, i32, P, P, P]),
             "orc_dequant": (None, [P, P, i32, i32, P]),
             "orc_residual_rmsnorm": (None, [P, P, P, i32, i32, f32, P]),
+            "orc_rms_sum": (f32, [P, i32]),
+            "orc_rmsnorm_cn": (None, [P, P, i32, i32, f32, f32, f32, i32, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -130,6 +133,16 @@ def router_logits(x_bf16, w):
     R, K = x_bf16.shape; E = w.shape[0]
     out = np.empty((R, E), np.float32)
     lib().orc_router_logits(_p(x_bf16), _p(w), R, K, E, _p(out))
+    return out
+
+
+def router_logits_f32(x, w):
+    """router logits of fp32 rows (exact widenings of bf16 or f16) in the router's fixed order"""
+    x = _c(x, np.float32); w = _c(w, np.float32)
+    R, K = x.shape
+    E = w.shape[0]
+    out = np.empty((R, E), np.float32)
+    lib().orc_router_logits_f32(_p(x), _p(w), R, K, E, _p(out))
     return out
 
 
@@ -232,3 +245,18 @@ def residual_rmsnorm(r, a, w, eps):
     xn = np.empty((R, H), np.uint16)
     lib().orc_residual_rmsnorm(_p(r), _p(aa), _p(w), R, H, eps, _p(xn))
     return r, xn
+
+
+def rms_sum(v):
+    """the fp32 sum of squares of one row in the reference's rms_norm_kernel order"""
+    v = _c(v, np.float32)
+    return np.float32(lib().orc_rms_sum(_p(v), v.size))
+
+
+def rmsnorm_cn(v, w, eps, cbias=0.0, cscale=1.0, bf16=True):
+    """xn of residual rows v [R, H] (after the add) in the reference's rms_norm_kernel order: uint16 bf16 or f16 bits"""
+    v = _c(v, np.float32); w = _c(w, np.float32)
+    R, H = v.shape
+    xn = np.empty((R, H), np.uint16)
+    lib().orc_rmsnorm_cn(_p(v), _p(w), R, H, eps, cbias, cscale, int(bool(bf16)), _p(xn))
+    return xn

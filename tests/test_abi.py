@@ -277,3 +277,60 @@ def test_prefill_chunks_past_the_32_bit_offsets_are_refused():
     assert L.hmoe_moe4t_forward(p, p, p, p, p, 8, 1, 8, *([p] * 10), 8, None, big, _lib.XF_BF16, None, 8, None) == 1
     assert b"4 GB" in L.hmoe_last_error()
     assert L.hmoe_moe4t_gemm(p, big, p, 1, 8, p, p, p, p, p, big, 0, None) == 1 and b"4 GB" in L.hmoe_last_error()
+    # the shared expert's dense GEMMs (the long prefill runs them before moe4t's own check)
+    assert L.hmoe_shared_forward(p, big, p, p, p, p, p, _lib.XF_BF16, None) == 1 and b"4 GB" in L.hmoe_last_error()
+
+
+def test_norm_entries_refuse_bad_arguments():
+    """combine_norm / norm_route / decode_combine_norm check their arguments before any GPU call: the RTX band's DONE
+    flag, the band hand-off words, dtype codes, row counts and alignment are refused with a message (a fake device
+    address is never dereferenced: every case fails a check first)"""
+    L = _lib.lib()
+    A = 1 << 20                                             # an aligned stand-in address (never read)
+    F32, BF16, F16 = 0, 1, 2
+    # combine_norm(f, o, y, rows, o2, done, r, w, xn, eps, cbias, cscale, w_dtype, xn_dtype, stream)
+    assert L.hmoe_combine_norm(A, None, A, 2, None, A, A, A, A, 1e-5, 0.0, 1.0, F16, F16, None) != 0
+    assert b"DONE" in L.hmoe_last_error()
+    assert L.hmoe_combine_norm(A, None, None, 2, None, None, A, A, A, 1e-5, 0.0, 1.0, F16, F16, None) != 0
+    assert L.hmoe_combine_norm(A, None, A, 65, None, None, A, A, A, 1e-5, 0.0, 1.0, F16, F16, None) != 0
+    assert b"rows" in L.hmoe_last_error()
+    assert L.hmoe_combine_norm(A, None, A, 2, None, None, A, A, A, 1e-5, 0.0, 1.0, 7, F16, None) != 0
+    assert b"dtype" in L.hmoe_last_error()
+    assert L.hmoe_combine_norm(A, None, A, 2, None, None, A, A, A, 1e-5, 0.0, 1.0, F16, F32, None) != 0
+    assert L.hmoe_combine_norm(A + 4, None, A, 2, None, None, A, A, A, 1e-5, 0.0, 1.0, F16, F16, None) != 0
+    assert b"alignment" in L.hmoe_last_error()
+    # norm_route(y, r, w, x2, gt, bias, sel, rw, cand, ctr, scale, eps, cbias, cscale, ho, n_ho, R, E, wdt, xdt, gdt, st)
+    ho = (ctypes.c_int64 * 10)(*range(10))
+    assert L.hmoe_norm_route(A, A, A, A, A, None, A, A, A, A, 2.5, 1e-5, 0.0, 1.0, ho, 10, 4, 256, F16, F16, F16,
+                             None) != 0
+    assert b"hand-off" in L.hmoe_last_error()
+    assert L.hmoe_norm_route(A, A, A, A, A, None, A, A, A, A, 2.5, 1e-5, 0.0, 1.0, None, 0, 17, 256, F16, F16, F16,
+                             None) != 0
+    assert L.hmoe_norm_route(A, A, A, A, A, None, A, A, A, A, 2.5, 1e-5, 0.0, 1.0, None, 0, 4, 257, F16, F16, F16,
+                             None) != 0
+    assert L.hmoe_norm_route(A, A, A, A, A, None, A, A, A, A, 2.5, 1e-5, 0.0, 1.0, None, 0, 4, 256, F16, F16, BF16,
+                             None) != 0
+    assert b"gate dtype" in L.hmoe_last_error()
+    assert L.hmoe_norm_route(A, A, A, A, A, None, A, A, None, A, 2.5, 1e-5, 0.0, 1.0, None, 0, 4, 256, F16, F16, F16,
+                             None) != 0
+    assert L.hmoe_norm_route_scratch_bytes(8, 256) == 8 * 256 * 4
+    # decode_combine_norm(y32, ctr, R, r, w, xn, xh, eps, cbias, cscale, wdt, xdt, st)
+    assert L.hmoe_decode_combine_norm(None, A, 4, A, A, A, None, 1e-5, 0.0, 1.0, F32, BF16, None) != 0
+    assert L.hmoe_decode_combine_norm(A, A, 17, A, A, A, None, 1e-5, 0.0, 1.0, F32, BF16, None) != 0
+
+
+def test_norm_mirrors_check_before_calling():
+    """the Python mirrors refuse host tensors, a non-empty hand-off and wrong dtypes before calling the library"""
+    import torch
+    from hecate_amd import cn, router
+    y = torch.zeros(2, 6144)
+    with pytest.raises(RuntimeError, match="device"):
+        cn.combine_norm(y, 0, y, 2, 0, 0, y, torch.zeros(6144, dtype=torch.float16), torch.zeros(2, 6144,
+                        dtype=torch.float16), 1e-5)
+    with pytest.raises(RuntimeError, match="device"):
+        router.norm_route(y, y, torch.zeros(6144), torch.zeros(2, 6144, dtype=torch.float16), torch.zeros(256, 6144),
+                          None, torch.zeros(2, 8, dtype=torch.int64), torch.zeros(2, 8, dtype=torch.float16),
+                          torch.zeros(2048), torch.zeros(64, dtype=torch.int32), 2.5, 1e-5)
+    with pytest.raises(RuntimeError, match="dtype"):
+        _lib.dt_of(torch.zeros(1, dtype=torch.int32))
+    assert _lib.dt_of(torch.zeros(1, dtype=torch.float16)) == 2 and _lib.dt_of(torch.zeros(1)) == 0

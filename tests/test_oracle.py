@@ -9,7 +9,8 @@
   pick_groups      brute-force block enumeration; hecate_amd.tier.pick_groups; invariants
   expert layer     numpy fp64 GEMVs on dequantised weights (tiny shapes); q8_0 mode: a many-pick job equals the sum
                    of its one-pick jobs bit for bit (tools/dev/test_grace_picks.py:63-80) and stays near the exact mode
-  rmsnorm          fp64 within one bf16 ulp; the fixed fp32 order emulated exactly with Fractions
+  rmsnorm          fp64 within one bf16 / f16 ulp (cbias, cscale); the reference's rms_norm_kernel tree restated with
+                   numpy arrays and exact fmaf, bit for bit, and shown to differ from other orders
 Nothing is unpinned: every oracle function used by the GPU parity tests has at least one of these checks.
 """
 from fractions import Fraction
@@ -88,8 +89,17 @@ def test_scales_are_abs_normal_bf16():
 # ---- router -------------------------------------------------------------------------------------------------------
 
 def _fma32(a, b, c):
-    """exact single-rounding fmaf through Fractions"""
-    return np.float32(float(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))))
+    """exact single-rounding fmaf through Fractions: the exact value rounded to fp32 once (a value that the rounding
+    to fp64 puts on an fp32 midpoint is resolved against the exact value, so no double rounding)"""
+    ex = Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))
+    d = float(ex)
+    f = np.float32(d)
+    if Fraction(float(f)) != ex and f != 0 and np.isfinite(f):
+        lo, hi = sorted((f, np.nextafter(f, np.float32(np.inf) if Fraction(float(f)) < ex else np.float32(-np.inf))))
+        mid = (Fraction(float(lo)) + Fraction(float(hi))) / 2
+        if ex != mid:
+            f = lo if ex < mid else hi
+    return np.float32(f)
 
 
 def test_router_logits_bound_and_exact_order():
@@ -341,32 +351,87 @@ def test_q8_many_picks_equal_sum_of_one_pick_jobs():
 
 # ---- rmsnorm ------------------------------------------------------------------------------------------------------
 
+def _rms_tree_numpy(v):
+    """the reference's rms_norm_kernel order restated with numpy arrays (a structure of its own, not the oracle's loops):
+    chains [1024] over float4 columns t, t + 1024, ...; the xor butterfly of each 32-lane group as whole-array steps;
+    the 32 group sums by the same steps"""
+    C = v.size // 4
+    cols = v.reshape(C, 4)
+    chains = []
+    for t in range(1024):
+        p = np.float32(0)
+        for c in range(t, C, 1024):
+            for e in range(4):
+                p = _fma32(cols[c, e], cols[c, e], p)
+        chains.append(p)
+    s = np.array(chains, np.float32).reshape(32, 32)
+    idx = np.arange(32)
+    for o in (16, 8, 4, 2, 1):
+        s = (s + s[:, idx ^ o]).astype(np.float32)
+    g = s[:, 0].copy()
+    for o in (16, 8, 4, 2, 1):
+        g = (g + g[idx ^ o]).astype(np.float32)
+    assert np.all(g == g[0]) and np.all(s == s[:, :1])          # every lane holds its butterfly's sum
+    return g[0]
+
+
 def test_rmsnorm_fp64_and_exact_order():
+    """residual + RMSNorm in the reference's order (cn.cu:21-31,80-103): fp64 within one bf16 ulp; the reduction tree
+    of rms_norm_kernel restated with numpy arrays, bit for bit; r = a + r"""
     rng = np.random.default_rng(10)
-    H = 512
-    r = rng.standard_normal((2, H)).astype(np.float32)
+    H = 6144
+    r = rng.standard_normal((2, H)).astype(np.float32) * 3
     a = rng.standard_normal((2, H)).astype(np.float32)
     w = (1 + 0.02 * rng.standard_normal(H)).astype(np.float32)
     r2, xn = O.residual_rmsnorm(r, a, w, 1e-5)
-    assert np.array_equal(r2, (r + a).astype(np.float32))
+    assert np.array_equal(r2, (a + r).astype(np.float32))
     v = (r + a).astype(np.float64)
     ref = v / np.sqrt((v ** 2).mean(1, keepdims=True) + 1e-5) * w
     assert np.all(np.abs(O.bf16_to_f32(xn) - ref) <= np.abs(ref) * 2 ** -8 + 1e-7)
-    vf = (r + a).astype(np.float32)[0]
-    part = []
-    for t in range(256):
-        p = np.float32(0)
-        for k in range(t, H, 256):
-            p = _fma32(vf[k], vf[k], p)
-        part.append(p)
-    off = 128
-    while off:
-        for t in range(off):
-            part[t] = np.float32(part[t] + part[t + off])
-        off >>= 1
-    rmf = np.float32(np.float32(1) / np.sqrt(np.float32(part[0] / np.float32(H)) + np.float32(1e-5), dtype=np.float32))
-    exp = O.f32_to_bf16(((vf * rmf).astype(np.float32) * w).astype(np.float32))
+    vf = (a + r).astype(np.float32)[0]
+    tot = _rms_tree_numpy(vf)
+    assert O.rms_sum(vf).view(np.uint32) == tot.view(np.uint32)
+    rmf = np.float32(np.float32(1) / np.sqrt(np.float32(tot / np.float32(H)) + np.float32(1e-5), dtype=np.float32))
+    exp = O.f32_to_bf16(((vf * w).astype(np.float32) * rmf).astype(np.float32))
     assert np.array_equal(xn[0], exp)
+
+
+def test_rmsnorm_cn_options_and_order_sensitivity():
+    """cbias / cscale / f16 out against fp64 (cn.cu:89,95-96: w + cbias only when cbias != 0, rmf scaled by cscale);
+    a sequential sum and a 256-chain fold give other bits on some rows, the tree's numpy restatement the oracle's on
+    every row (so the order is pinned, not only the value); a short row (H = 512: threads past H / 4 hold empty
+    chains) in the same order"""
+    rng = np.random.default_rng(11)
+    H = 6144
+    v = (rng.standard_normal((6, H)) * np.array([[1], [10], [0.01], [300], [1], [2]])).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(H)).astype(np.float32)
+    for cbias, cscale, bf in ((0.0, 1.0, True), (0.25, 1.0, False), (0.0, 0.5, False), (-0.5, 2.0, True)):
+        xn = O.rmsnorm_cn(v, w, 1e-6, cbias, cscale, bf)
+        got = O.bf16_to_f32(xn) if bf else O.f16_to_f32(xn)
+        vd = v.astype(np.float64)
+        ref = vd / np.sqrt((vd ** 2).mean(1, keepdims=True) + 1e-6) * (w.astype(np.float64) + cbias) * cscale
+        tol = np.abs(ref) * (2 ** -8 if bf else 2 ** -11) + 1e-6
+        assert np.all(np.abs(got - ref) <= tol), (cbias, cscale, bf)
+    differ_seq = differ_256 = 0
+    for row in v:
+        tot = _rms_tree_numpy(row)
+        assert O.rms_sum(row).view(np.uint32) == tot.view(np.uint32)
+        seq = np.float32(0)
+        for x in row:
+            seq = _fma32(x, x, seq)
+        part = [np.float32(0)] * 256
+        for k in range(H):
+            part[k % 256] = _fma32(row[k], row[k], part[k % 256])
+        off = 128
+        while off:
+            for t in range(off):
+                part[t] = np.float32(part[t] + part[t + off])
+            off >>= 1
+        differ_seq += seq != tot
+        differ_256 += part[0] != tot
+    assert differ_seq > 0 and differ_256 > 0
+    short = rng.standard_normal(512).astype(np.float32)
+    assert O.rms_sum(short).view(np.uint32) == _rms_tree_numpy(short).view(np.uint32)
 
 
 def test_bf16_ulp_is_the_spacing_of_bf16():
