@@ -434,28 +434,42 @@ def cpu_baseline():
     setup_s = time.perf_counter() - t_setup
     log(f"[bench] cpu baseline: {len(cache)} experts generated in {setup_s:.1f} s, {threads} pool threads on cores "
         f"{cores[0]}..{cores[-1]}")
-    # pool jobs, each run 3 times (the median kept)
+    # each config's sample is timed in rounds (a round = every sampled job of the config once) until at least MIN_S of
+    # work and MIN_ROUNDS rounds; the median round is kept and the spread (10th to 90th percentile over the median)
+    # reported, so the figure is stable from run to run
+    MIN_S, MIN_ROUNDS = 0.12, 5
+
+    def rounds_of(fn, items):
+        fn(*items[0])                                        # untimed: caches, pages, thread wake-up
+        out = []
+        while len(out) < MIN_ROUNDS or sum(out) < MIN_S:
+            out.append(sum(fn(*it) for it in items))
+        return out
     tier = CpuTier(threads=threads, first_core=cores[0] if info["pinned"] else -1, mapped=False)
     pool_s = {}
+    # the posting thread waits on a core outside the pool's (when there is one), so no pool thread shares its core
+    allowed = sorted(os.sched_getaffinity(0))
+    spare = [c for c in allowed if c not in set(cores)]
+    if spare:
+        os.sched_setaffinity(0, {spare[0]})
     try:
         for pl, ex in layers.items():
             tier.add_layer(pl, 0, ex)
 
         def run(pl, x, sel, rw):
-            best = []
-            for _ in range(3):
-                t0 = time.perf_counter()
-                tier.post(x, sel, rw, pl)
-                _, err = tier.wait()
-                best.append(time.perf_counter() - t0)
-                if err:
-                    raise RuntimeError(f"cpu baseline: job error {err}")
-            return float(np.median(best))
+            t0 = time.perf_counter()
+            tier.post(x, sel, rw, pl)
+            _, err = tier.wait()
+            el = time.perf_counter() - t0
+            if err:
+                raise RuntimeError(f"cpu baseline: job error {err}")
+            return el
         for cfg, js in jobs.items():
-            pool_s[cfg] = [run(*j) for j in js]
-        pool_s["config4_stack_b4"] = [run(pl, xn, sel, rw) for (pl, xn, sel, rw, _) in stack]
+            pool_s[cfg] = rounds_of(run, js)
+        pool_s["config4_stack_b4"] = rounds_of(run, [(pl, xn, sel, rw) for (pl, xn, sel, rw, _) in stack])
     finally:
         tier.close()
+        os.sched_setaffinity(0, set(allowed))
 
     # router (fp32 logits, sigmoid + bias top-8) and shared expert (bf16 weights and activations, fp32 accumulation)
     # through torch's CPU GEMMs on the same number of threads, the pool stopped
@@ -487,30 +501,36 @@ def cpu_baseline():
     # one untimed call per weight set first: torch's first CPU GEMM creates its thread pool and kernel caches
     for hl in [hl0, hl3] + [s[4] for s in stack]:
         router_shared(hl, x0[0], hl.shared is not None)
-    r_s["config0_b1"] = [router_shared(hl0, x) for x in x0]
-    r_s["config1_b16_zipf"] = [router_shared(hl0, x16)]
+    r_s["config0_b1"] = rounds_of(router_shared, [(hl0, x) for x in x0])
+    r_s["config1_b16_zipf"] = rounds_of(router_shared, [(hl0, x16)])
     for B in (1, 4, 8):
-        r_s[f"config3_b{B}"] = [router_shared(hl3, np.concatenate(x0[:B]), False)]
-    r_s["config2_prefill_8row_jobs"] = [router_shared(hl0, x2)]
-    r_s["config4_stack_b4"] = [router_shared(hl, xn) for (_, xn, _, _, hl) in stack]
+        r_s[f"config3_b{B}"] = rounds_of(router_shared, [(hl3, np.concatenate(x0[:B]), False)])
+    r_s["config2_prefill_8row_jobs"] = rounds_of(router_shared, [(hl0, x2)])
+    r_s["config4_stack_b4"] = rounds_of(router_shared, [(hl, xn) for (_, xn, _, _, hl) in stack])
     res = {}
     for cfg in pool_s:
-        p, r = float(np.sum(pool_s[cfg])), float(np.sum(r_s[cfg]))
+        pr, rr = np.array(pool_s[cfg]), np.array(r_s[cfg])
+        p, r = float(np.median(pr)), float(np.median(rr))
         rows = {"config0_b1": 8, "config1_b16_zipf": 16, "config3_b1": 1, "config3_b4": 4, "config3_b8": 8,
                 "config2_prefill_8row_jobs": 8, "config4_stack_b4": 4}[cfg]
         n_steps = {"config0_b1": 8}.get(cfg, 1)
         step = (p + r) / n_steps
         if cfg == "config4_stack_b4":
             step = step * 16 / 4                             # 4 of the 16 layers sampled
+        spread = lambda a: float((np.percentile(a, 90) - np.percentile(a, 10)) / np.median(a))
         res[cfg] = {"us_per_step": step * 1e6, "tok_per_s": (rows / n_steps) / step,
-                    "pool_us": p / n_steps * 1e6, "router_shared_us": r / n_steps * 1e6}
+                    "pool_us": p / n_steps * 1e6, "router_shared_us": r / n_steps * 1e6,
+                    "rounds": [len(pr), len(rr)], "timed_s": float(pr.sum() + rr.sum()),
+                    "spread_p10_p90": [spread(pr), spread(rr)]}
     res["config2_prefill_8row_jobs"]["ms_per_2048_chunk"] = res["config2_prefill_8row_jobs"]["us_per_step"] * 256 / 1e3
     head = res["config0_b1"]
     info.update({"setup_s": setup_s, "experts_generated": len(cache)})
     return {"value": head["tok_per_s"], "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": (f"config 0 (B = 1): 8 tokens of layer 0 (one 1-row job of the restated cpuband path on the "
-                       f"pinned pool, the median of 3 runs, + router and bf16 shared expert on torch's CPU GEMMs) on "
-                       f"{info['cpu_model']}, {threads} threads from core {cores[0]}; per-config figures in configs"),
+            "sample": (f"config 0 (B = 1): 8 tokens of layer 0 (one 1-row job each of the restated cpuband path on "
+                       f"the pinned pool, then router and bf16 shared expert on torch's CPU GEMMs), timed in rounds of "
+                       f"the 8 tokens until >= {MIN_S} s and {MIN_ROUNDS} rounds of each part, the median round kept; "
+                       f"{info['cpu_model']}, {threads} threads from core {cores[0]}; per-config figures, round counts "
+                       f"and spreads in configs"),
             "configs": res, "host": info}
 
 

@@ -23,6 +23,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <immintrin.h>
+#include <memory>
 #include <mutex>
 #include <sched.h>
 #include <thread>
@@ -41,30 +42,45 @@ struct Mat { const uint8_t* q = nullptr; const uint16_t* s = nullptr; };
 struct Expert { Mat gate, up, down; };
 struct Layer { int lo = 0; std::vector<Expert> ex; };
 
-// the job's work arrays (sized for CMAXR rows and up to CMAXR * TOPK picks)
+// the job's work arrays (sized for CMAXR rows and up to MAXP = CMAXR * TOPK picks)
+constexpr int MAXP = CMAXR * TOPK;
 struct Work
 {
     int P = 0, R = 0;
-    int32_t pick[CMAXR * TOPK];
-    float wgt[CMAXR * TOPK][CMAXR];
-    int nrows[CMAXR * TOPK], rows[CMAXR * TOPK][CMAXR];
+    const Layer* ly = nullptr;     // the job's layer (thread 0 reads it in the parse; the others after the barrier)
+    int32_t pick[MAXP];
+    float wgt[MAXP][CMAXR];
+    int nrows[MAXP], rows[MAXP][CMAXR];
     std::vector<int8_t> xq;        // [R][H]
     std::vector<float> xs;         // [R][H / 32]
-    std::vector<float> gy, uy;     // [R][I] of the current pick
-    std::vector<int8_t> aq;        // [P][R][I]
-    std::vector<float> as;         // [P][R][I / 32]
-    Work() : xq(CMAXR * H), xs(CMAXR * H / 32), gy(CMAXR * I), uy(CMAXR * I), aq((size_t) CMAXR * TOPK * CMAXR * I),
-             as((size_t) CMAXR * TOPK * CMAXR * I / 32) {}
+    std::vector<int8_t> xqp;       // [P][CMAXR][H]: each pick's rows of xq, compacted
+    std::vector<float> xsp;        // [P][CMAXR][H / 32]
+    std::vector<float> gy, uy;     // [P][CMAXR][I]
+    std::vector<int8_t> aq;        // [P][CMAXR][I]
+    std::vector<float> as;         // [P][CMAXR][I / 32]
+    Work() : xq(CMAXR * H), xs(CMAXR * H / 32), xqp((size_t) MAXP * CMAXR * H), xsp((size_t) MAXP * CMAXR * H / 32),
+             gy((size_t) MAXP * CMAXR * I), uy((size_t) MAXP * CMAXR * I), aq((size_t) MAXP * CMAXR * I),
+             as((size_t) MAXP * CMAXR * I / 32) {}
 };
+
+constexpr int MAX_LAYERS = 4097;                     // layer ids 0 .. 4096
+constexpr int MAX_THREADS = 256;
 
 struct Pool
 {
     std::vector<std::thread> th;
-    std::vector<Layer> layers;
+    // the layers, each published once complete through an atomic pointer and never changed after (add_layer of an id
+    // that exists publishes a new record; the old ones are kept until the pool stops), so a job that reads a layer
+    // while the host adds another (or replaces this one) reads a whole, unchanging record
+    std::atomic<const Layer*> layer[MAX_LAYERS];
+    std::vector<std::unique_ptr<Layer>> owned;        // every record published (freed at stop)
     hmoe_cpu_mailbox* mb = nullptr;
     std::atomic<int> stop{0};
-    alignas(128) std::atomic<int> bar_count{0};      // (counter and generation on their own lines)
-    alignas(128) std::atomic<int> bar_gen{0};
+    // gather barrier (cpuband.cpp:62-75): thread t > 0 releases its own 128-byte line with its barrier count, thread
+    // 0 acquires them all and releases the sense line; no line is written by more than one thread
+    struct alignas(128) Flag { std::atomic<uint32_t> v{0}; };
+    Flag flag[MAX_THREADS];
+    alignas(128) std::atomic<uint32_t> sense{0};
     int nthr = 0;
     uint32_t start_gen = 0;                           // the mailbox's issue at start: taken as served
     bool skip = false;                                // HMOE_CPU_SKIP: acknowledge jobs with a zero partial
@@ -76,18 +92,25 @@ struct Pool
 static Pool* g_pool = nullptr;
 static std::mutex g_mu;
 
-// barrier for the pool's threads (sense by generation); false when the pool is stopping (a thread that never arrives,
-// e.g. one held back or gone, must not keep the others here past hmoe_cpu_stop)
-static bool barrier(Pool& p)
+// the pool's barrier: gen is the calling thread's own count of barriers passed (every thread passes the same
+// sequence, so the counts agree); false when the pool is stopping (a thread that never arrives, e.g. one held back or
+// gone, must not keep the others here past hmoe_cpu_stop)
+static bool barrier(Pool& p, int t, uint32_t& gen)
 {
-    const int gen = p.bar_gen.load(std::memory_order_acquire);
-    if (p.bar_count.fetch_add(1, std::memory_order_acq_rel) + 1 == p.nthr)
+    ++gen;
+    if (t == 0)
     {
-        p.bar_count.store(0, std::memory_order_relaxed);
-        p.bar_gen.store(gen + 1, std::memory_order_release);
+        for (int i = 1; i < p.nthr; ++i)
+            while (p.flag[i].v.load(std::memory_order_acquire) != gen)
+            {
+                if (p.stop.load(std::memory_order_acquire)) return false;
+                _mm_pause();
+            }
+        p.sense.store(gen, std::memory_order_release);
         return true;
     }
-    while (p.bar_gen.load(std::memory_order_acquire) == gen)
+    p.flag[t].v.store(gen, std::memory_order_release);
+    while (p.sense.load(std::memory_order_acquire) != gen)
     {
         if (p.stop.load(std::memory_order_acquire)) return false;
         _mm_pause();
@@ -236,20 +259,26 @@ static void range(int total, int t, int T, int& a, int& b)
     b = (int) ((long long) total * (t + 1) / T);
 }
 
-// one job (generation g), by every thread of the pool (t = 0 .. nthr - 1); false when the pool stopped inside it
-static bool run_job(Pool& p, int t, uint32_t g)
+// one job (generation g), by every thread of the pool (t = 0 .. nthr - 1), in the phases of cpuband.cpp:137-218, each
+// ended by a barrier: thread 0 parses the picks while the others quantise every row of x (:137-179), then the rows of
+// each pick are gathered, the gate and up rows of every pick are split over the threads (one phase for all picks), the
+// activations are quantised, and the down rows are split (each output summed over the picks in order). False when the
+// pool stopped inside it.
+static bool run_job(Pool& p, int t, uint32_t g, uint32_t& gen)
 {
     hmoe_cpu_mailbox* mb = p.mb;
     Work& w = p.w;
     const int T = p.nthr;
+    const int R0 = mb->rows, L0 = mb->layer;
+    const bool rows_ok = R0 >= 1 && R0 <= CMAXR;
     if (t == 0)
     {
-        const int R = mb->rows, L = mb->layer;
-        w.R = (R >= 1 && R <= CMAXR) ? R : 0;
+        w.R = rows_ok ? R0 : 0;
         w.P = 0;
-        if (w.R && !p.skip && L >= 0 && L < (int) p.layers.size())
+        w.ly = (w.R && L0 >= 0 && L0 < MAX_LAYERS) ? p.layer[L0].load(std::memory_order_acquire) : nullptr;
+        if (w.ly && !p.skip)
         {
-            const Layer& ly = p.layers[L];
+            const Layer& ly = *w.ly;
             const int n = (int) ly.ex.size();
             for (int i = 0; i < w.R * TOPK; ++i)
             {
@@ -268,13 +297,11 @@ static bool run_job(Pool& p, int t, uint32_t g)
             }
         }
     }
-    if (!barrier(p)) return false;
-    const int R = w.R, P = w.P;
-    const Layer* ly = (R && mb->layer >= 0 && mb->layer < (int) p.layers.size()) ? &p.layers[mb->layer] : nullptr;
-    // q8_0 of every row of x
+    // q8_0 of every row of x, by threads 1 .. T - 1 (all of it by thread 0 when it is alone)
+    if (rows_ok && (t != 0 || T == 1))
     {
         int a, b;
-        range(R * H / 32, t, T, a, b);
+        range(R0 * H / 32, T == 1 ? 0 : t - 1, T == 1 ? 1 : T - 1, a, b);
         for (int gi = a; gi < b; ++gi)
         {
             float v[32];
@@ -282,53 +309,74 @@ static bool run_job(Pool& p, int t, uint32_t g)
             quant_group(v, w.xq.data() + (size_t) gi * 32, w.xs.data() + gi);
         }
     }
-    if (!barrier(p)) return false;
-    // per pick: gate / up over the pick's rows, then act -> q8_0
-    static thread_local std::vector<int8_t> xqp(CMAXR * H);
-    static thread_local std::vector<float> xsp(CMAXR * H / 32);
-    for (int q = 0; q < P; ++q)
+    if (!barrier(p, t, gen)) return false;
+    const int R = w.R, P = w.P;
+    if (R && P)
     {
-        const Expert& ex = ly->ex[w.pick[q]];
-        const int nr = w.nrows[q];
-        for (int j = 0; j < nr; ++j)
+        const Layer& ly = *w.ly;
+        // each pick's rows of x, compacted
         {
-            const int r = w.rows[q][j];
-            std::memcpy(xqp.data() + (size_t) j * H, w.xq.data() + (size_t) r * H, H);
-            std::memcpy(xsp.data() + (size_t) j * (H / 32), w.xs.data() + (size_t) r * (H / 32), sizeof(float) * (H / 32));
-        }
-        int a, b;
-        range(I, t, T, a, b);
-        gemv_any(ex.gate, H, xqp.data(), xsp.data(), nr, a, b, w.gy.data(), I);
-        gemv_any(ex.up, H, xqp.data(), xsp.data(), nr, a, b, w.uy.data(), I);
-        if (!barrier(p)) return false;
-        range(nr * I / 32, t, T, a, b);
-        for (int gi = a; gi < b; ++gi)
-        {
-            const int j = gi / (I / 32), k0 = (gi % (I / 32)) * 32;
-            const float wt = w.wgt[q][w.rows[q][j]];
-            float v[32];
-            for (int k = 0; k < 32; ++k)
+            int a, b;
+            range(P * CMAXR, t, T, a, b);
+            for (int i = a; i < b; ++i)
             {
-                const float gg = w.gy[(size_t) j * I + k0 + k];
-                v[k] = gg / (1.0f + expf(-gg)) * w.uy[(size_t) j * I + k0 + k] * wt;
+                const int q = i / CMAXR, j = i % CMAXR;
+                if (j >= w.nrows[q]) continue;
+                const int r = w.rows[q][j];
+                std::memcpy(w.xqp.data() + ((size_t) q * CMAXR + j) * H, w.xq.data() + (size_t) r * H, H);
+                std::memcpy(w.xsp.data() + ((size_t) q * CMAXR + j) * (H / 32), w.xs.data() + (size_t) r * (H / 32),
+                            sizeof(float) * (H / 32));
             }
-            quant_group(v, w.aq.data() + ((size_t) q * CMAXR + j) * I + k0,
-                        w.as.data() + (((size_t) q * CMAXR + j) * I + k0) / 32);
         }
-        if (!barrier(p)) return false;
+        if (!barrier(p, t, gen)) return false;
+        // gate and up rows of every pick: the (pick, matrix, row) range split over the threads
+        {
+            int a, b;
+            range(P * 2 * I, t, T, a, b);
+            for (int i = a; i < b;)
+            {
+                const int q = i / (2 * I), m = (i / I) % 2, n0 = i % I, n1 = std::min(I, n0 + (b - i));
+                const Expert& ex = ly.ex[w.pick[q]];
+                gemv_any(m ? ex.up : ex.gate, H, w.xqp.data() + (size_t) q * CMAXR * H,
+                         w.xsp.data() + (size_t) q * CMAXR * (H / 32), w.nrows[q], n0, n1,
+                         (m ? w.uy : w.gy).data() + (size_t) q * CMAXR * I, I);
+                i += n1 - n0;
+            }
+        }
+        if (!barrier(p, t, gen)) return false;
+        // act = silu(g) u wgt -> q8_0, every pick's rows
+        {
+            int a, b;
+            range(P * CMAXR * (I / 32), t, T, a, b);
+            for (int gi = a; gi < b; ++gi)
+            {
+                const int q = gi / (CMAXR * (I / 32)), j = (gi / (I / 32)) % CMAXR, k0 = (gi % (I / 32)) * 32;
+                if (j >= w.nrows[q]) continue;
+                const float wt = w.wgt[q][w.rows[q][j]];
+                const size_t o = ((size_t) q * CMAXR + j) * I + k0;
+                float v[32];
+                for (int k = 0; k < 32; ++k)
+                {
+                    const float gg = w.gy[o + k];
+                    v[k] = gg / (1.0f + expf(-gg)) * w.uy[o + k] * wt;
+                }
+                quant_group(v, w.aq.data() + o, w.as.data() + o / 32);
+            }
+        }
+        if (!barrier(p, t, gen)) return false;
     }
-    // down: output rows split over the threads, picks in order, summed into out from 0
+    // down: output rows split over the threads, picks in order, summed into out from 0 (out zero when no pick runs)
     {
         int a, b;
         range(H, t, T, a, b);
         for (int r = 0; r < R; ++r) std::memset(mb->out + (size_t) r * H + a, 0, sizeof(float) * (size_t) (b - a));
         static thread_local std::vector<float> y1(CMAXR * H);
-        for (int q = 0; q < P; ++q)
+        for (int q = 0; q < (R ? P : 0); ++q)
         {
-            const Expert& ex = ly->ex[w.pick[q]];
+            const Expert& ex = w.ly->ex[w.pick[q]];
             const int nr = w.nrows[q];
             gemv_any(ex.down, I, w.aq.data() + (size_t) q * CMAXR * I, w.as.data() + (size_t) q * CMAXR * I / 32, nr, a, b,
-                 y1.data(), H);
+                     y1.data(), H);
             for (int j = 0; j < nr; ++j)
             {
                 float* o = mb->out + (size_t) w.rows[q][j] * H;
@@ -336,12 +384,12 @@ static bool run_job(Pool& p, int t, uint32_t g)
             }
         }
     }
-    if (!barrier(p)) return false;
+    if (!barrier(p, t, gen)) return false;
     if (t == 0)
     {
         p.jobs.fetch_add(1, std::memory_order_relaxed);
         p.picks.fetch_add(P, std::memory_order_relaxed);
-        mb->err = !R ? 1 : (ly || p.skip ? 0 : 2);          // 1: bad row count, 2: no such layer
+        mb->err = !R ? 1 : (w.ly || p.skip ? 0 : 2);        // 1: bad row count, 2: no such layer
         __atomic_store_n(&mb->done, g, __ATOMIC_RELEASE);
     }
     return true;
@@ -357,6 +405,7 @@ static void worker(Pool* p, int t, int core)
         sched_setaffinity(0, sizeof(cs), &cs);       // best effort
     }
     int idle = 0;
+    uint32_t gen = 0;                                // barriers this thread has passed
     uint32_t last = p->start_gen;                    // the generation this thread served last
     while (true)
     {
@@ -370,7 +419,7 @@ static void worker(Pool* p, int t, int core)
         {
             idle = 0;
             last = g;
-            if (!run_job(*p, t, g)) return;
+            if (!run_job(*p, t, g, gen)) return;
             if (t == p->hold_t)
                 for (int us = 0; us < p->hold_us && !p->stop.load(std::memory_order_acquire); us += 1000)
                     std::this_thread::sleep_for(std::chrono::microseconds(std::min(1000, p->hold_us - us)));
@@ -391,13 +440,14 @@ extern "C" int hmoe_cpu_start(hmoe_cpu_mailbox* mb, int threads, int first_core)
 {
     std::lock_guard<std::mutex> lk(g_mu);
     if (g_pool) return hmoe::set_error(HMOE_ERR_ARG, "cpu_start: the pool is running");
-    if (!mb || threads < 1 || threads > 256) return hmoe::set_error(HMOE_ERR_ARG, "cpu_start: mailbox / threads");
+    if (!mb || threads < 1 || threads > MAX_THREADS) return hmoe::set_error(HMOE_ERR_ARG, "cpu_start: mailbox / threads");
     // the dot kernel: AVX-512 VNNI where the host has it, unless HMOE_CPU_ISA=avx2 asks for the AVX2 one (both give
     // the same bits)
     const char* isa = std::getenv("HMOE_CPU_ISA");
     g_vnni = __builtin_cpu_supports("avx512vnni") && __builtin_cpu_supports("avx512bw") &&
              !(isa && std::strcmp(isa, "avx2") == 0);
     Pool* p = new Pool();
+    for (auto& l : p->layer) l.store(nullptr, std::memory_order_relaxed);
     p->mb = mb;
     p->nthr = threads;
     p->start_gen = __atomic_load_n(&mb->issue, __ATOMIC_ACQUIRE);
@@ -415,25 +465,26 @@ extern "C" int hmoe_cpu_add_layer(int layer, int lo, int n, const uint8_t* const
 {
     std::lock_guard<std::mutex> lk(g_mu);
     if (!g_pool) return hmoe::set_error(HMOE_ERR_ARG, "cpu_add_layer: no pool");
-    if (layer < 0 || layer > 4096 || lo < 0 || n < 0 || n > 256 || (n && (!q || !s))) return hmoe::set_error(HMOE_ERR_ARG, "cpu_add_layer: arguments");
+    if (layer < 0 || layer >= MAX_LAYERS || lo < 0 || n < 0 || n > 256 || (n && (!q || !s)))
+        return hmoe::set_error(HMOE_ERR_ARG, "cpu_add_layer: arguments");
     hmoe_cpu_mailbox* mb = g_pool->mb;
     if (__atomic_load_n(&mb->issue, __ATOMIC_ACQUIRE) != __atomic_load_n(&mb->done, __ATOMIC_ACQUIRE))
         return hmoe::set_error(HMOE_ERR_ARG, "cpu_add_layer: a job is in flight");
     // every pointer is checked before the pool's layers change
     for (int i = 0; i < 3 * n; ++i)
         if (!q[i] || !s[i]) return hmoe::set_error(HMOE_ERR_ARG, "cpu_add_layer: null matrix (expert %d)", i / 3);
-    Layer L;
-    L.lo = lo;
-    L.ex.assign(n, Expert{});
+    std::unique_ptr<Layer> L(new Layer());
+    L->lo = lo;
+    L->ex.assign(n, Expert{});
     for (int e = 0; e < n; ++e)
     {
         // q / s: per expert the gate, up and down pointers (3 n each)
-        L.ex[e].gate = {q[3 * e + 0], s[3 * e + 0]};
-        L.ex[e].up = {q[3 * e + 1], s[3 * e + 1]};
-        L.ex[e].down = {q[3 * e + 2], s[3 * e + 2]};
+        L->ex[e].gate = {q[3 * e + 0], s[3 * e + 0]};
+        L->ex[e].up = {q[3 * e + 1], s[3 * e + 1]};
+        L->ex[e].down = {q[3 * e + 2], s[3 * e + 2]};
     }
-    if ((int) g_pool->layers.size() <= layer) g_pool->layers.resize(layer + 1);
-    g_pool->layers[layer] = std::move(L);
+    g_pool->layer[layer].store(L.get(), std::memory_order_release);
+    g_pool->owned.push_back(std::move(L));
     return 0;
 }
 

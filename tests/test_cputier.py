@@ -263,3 +263,41 @@ def test_add_layer_refusal_leaves_the_layer(hl, cold):
         assert err == 0 and np.array_equal(out.view(np.uint32), oracle_q8(hl, x, sel, rw).view(np.uint32))
     finally:
         t.close()
+
+
+def test_cpu_tier_layers_added_while_jobs_run(hl, cold):
+    """layers published to a serving pool (ids other than the job's, and the job's own id again with the same
+    experts) while jobs run back to back: every job keeps the oracle's bits (the pool reads a layer through one
+    atomically published, unchanging record, so a concurrent add never resizes or rewrites what a job reads)"""
+    import threading
+    t = start(cold, 4)
+    try:
+        R = 3
+        x = x_rows(909, R)
+        sel, rw = picks(R, 21)
+        ref = oracle_q8(hl, x, sel, rw)
+        done = threading.Event()
+        added = [0]
+
+        def adder():
+            k = 1
+            while not done.is_set():
+                try:
+                    t.add_layer(k % 50 + 1, LO, cold)         # refused while a job is in flight, else published
+                    added[0] += 1
+                except RuntimeError:
+                    pass
+                k += 1
+        th = threading.Thread(target=adder)
+        th.start()
+        try:
+            for _ in range(40):
+                t.post(x, sel, rw, 0)
+                out, err = t.wait()
+                assert err == 0 and np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+        finally:
+            done.set()
+            th.join()
+        assert added[0] > 0
+    finally:
+        t.close()
