@@ -8,7 +8,9 @@
   dispatch         numpy stable argsort + bincount (tier_split.py:405-412 itself); inverse map
   pick_groups      brute-force block enumeration; hecate_amd.tier.pick_groups; invariants
   expert layer     numpy fp64 GEMVs on dequantised weights (tiny shapes); q8_0 mode: a many-pick job equals the sum
-                   of its one-pick jobs bit for bit (tools/dev/test_grace_picks.py:63-80) and stays near the exact mode
+                   of its one-pick jobs bit for bit (tools/dev/test_grace_picks.py:63-80) and stays near the exact mode;
+                   its quantisation, nibble order and integer dot in closed form; its fp32 lane steps against ARM's
+                   published FMLA / FADDP semantics (a closed-form fold case and a fused-vs-unfused random case)
   rmsnorm          fp64 within one bf16 / f16 ulp (cbias, cscale); the reference's rms_norm_kernel tree restated with
                    numpy arrays and exact fmaf, bit for bit, and shown to differ from other orders
 Nothing is unpinned: every oracle function used by the GPU parity tests has at least one of these checks.
@@ -489,3 +491,95 @@ def test_q8_quantisation_and_integer_dot_in_closed_form():
     y_sw, _, _ = O.q8_gemv(np.ascontiguousarray(swapped[:, 0::2] | (swapped[:, 1::2] << 4)), scales, x)
     assert not np.array_equal(y_sw, y)
     assert not np.array_equal(np.round(qx * 127.0 / 128.0).astype(np.int64), q_exp)
+
+
+def _q8_model(packed, scales, xq, xg, fused=True, fold="pairwise"):
+    """cpuband.cpp:80-104 (with group-128 scales) from ARM's published semantics of its two float intrinsics:
+    vfmaq_n_f32 is FMLA, a fused multiply-add rounded once per lane and step; vaddvq_f32 over 4 lanes is FADDP twice,
+    (a0 + a1) + (a2 + a3). The int32 lane sums (vdotq_s32: lane i of a 32-block = k 4i..4i+3 and 16+4i..16+4i+3) by
+    numpy int64. fused=False (multiply, round, add, round) and the other folds are the alternatives the pins must tell
+    apart."""
+    N, K = packed.shape[0], packed.shape[1] * 2
+    nr = xq.shape[0]
+    codes = np.empty((N, K), np.int64)
+    codes[:, 0::2] = packed & 15
+    codes[:, 1::2] = packed >> 4
+    z = codes - 8
+    xr = xq.astype(np.int64)
+    nb = K // 32
+    # lane sums d[r][n][b][i]
+    zb = z.reshape(N, nb, 2, 4, 4)                 # [n][b][half][lane][j]
+    xb = xr.reshape(nr, nb, 2, 4, 4)
+    d = np.einsum("nbhij,rbhij->rnbi", zb, xb)
+    sc = O.bf16_to_f32(scales).astype(np.float32)
+    y = np.zeros((nr, N), np.float32)
+    for r in range(nr):
+        for n in range(N):
+            yr = np.float32(0)
+            for g in range(K // 128):
+                a = [np.float32(0)] * 4
+                for b in range(4 * g, 4 * g + 4):
+                    for i in range(4):
+                        dv, xv = np.float32(d[r, n, b, i]), xg[r, b]
+                        a[i] = _fma32(dv, xv, a[i]) if fused else np.float32(np.float32(dv * xv) + a[i])
+                if fold == "pairwise":
+                    f = np.float32(np.float32(a[0] + a[1]) + np.float32(a[2] + a[3]))
+                elif fold == "sequential":
+                    f = np.float32(np.float32(np.float32(a[0] + a[1]) + a[2]) + a[3])
+                elif fold == "02_13":
+                    f = np.float32(np.float32(a[0] + a[2]) + np.float32(a[1] + a[3]))
+                else:
+                    f = np.float32(np.float32(a[0] + a[3]) + np.float32(a[1] + a[2]))
+                yr = _fma32(sc[n, g], f, yr)
+            y[r, n] = yr
+    return y
+
+
+def test_q8_lane_fold_and_fused_steps_pinned():
+    """the q8_0 mode's fp32 steps, pinned to the published semantics of the reference's NEON intrinsics
+    (cpuband.cpp:96-101): a closed-form group whose four lanes hold (2^24, 1, 1, -2^24) and (2^24, 1, -2^24, 1)
+    exactly gives 1 under FADDP's (a0 + a1) + (a2 + a3) and 0 or 2 under the sequential, (a0 + a2) + (a1 + a3) and
+    (a0 + a3) + (a1 + a2) folds; on random data the oracle equals the fused per-lane model bit for bit and differs from
+    the multiply-then-add one"""
+    # closed form: K = 128 (one group of 4 blocks), 2 weight rows, 1 row of x
+    K = 128
+    xq_t = np.zeros(K, np.int64)
+    xe = np.zeros(4, np.int64)                   # block exponents: xg = 2^e when the absmax is 127 * 2^e
+    codes = np.full((2, K), 8, np.int64)         # code 8: z = 0
+    # block 0 (xg = 2^12): lane 0 of row 0 sums 8 x (-8)(-64) = 4096 -> 2^24; lane 3 of row 0 and lane 2 of row 1
+    # -4096 -> -2^24; row 1's lane 0 as row 0's
+    xe[0] = 12
+    for k in list(range(0, 4)) + list(range(16, 20)):
+        xq_t[k] = -64; codes[0, k] = 0; codes[1, k] = 0
+    for k in list(range(12, 16)) + list(range(28, 32)):
+        xq_t[k] = 64; codes[0, k] = 0
+    for k in list(range(8, 12)) + list(range(24, 28)):
+        xq_t[k] = 64; codes[1, k] = 0
+    xq_t[4] = 127                                # the block's absmax, at a z = 0 position (both rows)
+    # block 1 (xg = 2^-7): row 0 lanes 1, 2 and row 1 lanes 1, 3 sum (-8)(-16) = 128 -> 1
+    xe[1] = -7
+    for k, rows in ((32 + 4, (0, 1)), (32 + 8, (0,)), (32 + 12, (1,))):
+        xq_t[k] = -16
+        for n in rows:
+            codes[n, k] = 0
+    xq_t[32 + 17] = -127                         # the absmax
+    x = (xq_t.astype(np.float64) * np.exp2(np.repeat(np.concatenate([xe[:2], [0, 0]]), 32))).astype(np.float32)
+    x[64:] = 0.0                                 # blocks 2, 3 empty (scale 1, all codes contribute 0)
+    x = x[None, :]
+    packed = np.ascontiguousarray((codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8))
+    scales = O.f32_to_bf16(np.ones((2, 1), np.float32))
+    y, xq, xg = O.q8_gemv(packed, scales, x)
+    assert np.array_equal(xq[0].astype(np.int64), xq_t) and np.array_equal(xg[0], np.array([4096, 2 ** -7, 1, 1],
+                                                                                       np.float32))
+    assert np.array_equal(y, np.array([[1.0, 1.0]], np.float32))
+    for fold, exp in (("sequential", [0.0, 1.0]), ("02_13", [1.0, 2.0]), ("03_12", [2.0, 1.0])):
+        assert np.array_equal(_q8_model(packed, scales, xq, xg, fold=fold), np.array([exp], np.float32)), fold
+    # random data: the fused per-lane steps bit for bit, and the case has the power to see an unfused one
+    rng = np.random.default_rng(77)
+    N, K, nr = 12, 512, 3
+    x = (rng.standard_normal((nr, K)) * np.exp2(rng.integers(-3, 3, (nr, K)))).astype(np.float32)
+    packed = rng.integers(0, 256, (N, K // 2)).astype(np.uint8)
+    scales = O.f32_to_bf16(np.abs(rng.standard_normal((N, K // 128)) * 0.01).astype(np.float32))
+    y, xq, xg = O.q8_gemv(packed, scales, x)
+    assert np.array_equal(y.view(np.uint32), _q8_model(packed, scales, xq, xg).view(np.uint32))
+    assert not np.array_equal(y, _q8_model(packed, scales, xq, xg, fused=False))
