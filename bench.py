@@ -209,14 +209,23 @@ def tiered_workload(torch, synth, steps, warmup, dev, threads=8):
     import numpy as np
     from hecate_amd.cpu_tier import CpuTier, decode_split, host_experts
     lay = synth.make_layer(0, dev, resident=synth.popularity_order()[:176], shared=False)
-    cpu = CpuTier(threads=threads)
+    # the pool pinned to the CPU baseline's cores (the reference pins its workers, tier_split.py:35-36) and this
+    # thread, which waits on the GPU, kept off them
+    cores, info = cpu_cores()
+    threads = min(threads, len(cores))
+    cpu = CpuTier(threads=threads, first_core=cores[0] if info["pinned"] else -1)
+    allowed = sorted(os.sched_getaffinity(0))
+    spare = [c for c in allowed if c not in set(cores[:threads])]
+    if spare:
+        os.sched_setaffinity(0, set(spare))
     try:
         with open("/proc/cpuinfo") as f:
             flags = next((ln for ln in f if ln.startswith("flags")), "").split()
     except OSError:
         flags = []
     vnni = "avx512_vnni" in flags and "avx512bw" in flags and os.environ.get("HMOE_CPU_ISA") != "avx2"
-    out = {"cpu_threads": threads, "cpu_dot": "avx512-vnni" if vnni else "avx2"}
+    out = {"cpu_threads": threads, "cpu_dot": "avx512-vnni" if vnni else "avx2",
+           "first_core": cores[0] if info["pinned"] else None}
     try:
         cpu.add_layer(0, 176, host_experts(0, lay.perm[176:], dev))
         for R in (1, 4, 8):
@@ -235,6 +244,7 @@ def tiered_workload(torch, synth, steps, warmup, dev, threads=8):
     finally:
         torch.cuda.synchronize()
         cpu.close()
+        os.sched_setaffinity(0, set(allowed))
     del lay
     torch.cuda.empty_cache()
     return out
