@@ -207,7 +207,8 @@ def tiered_workload(torch, synth, steps, warmup, dev, threads=8):
     rows to the pool through the device-mapped mailbox, run the 176 resident experts into the fp32 partial
     meanwhile, then add the pool's partial on the same stream; one layer, 32 seeded inputs per row count"""
     import numpy as np
-    from hecate_amd.cpu_tier import CpuTier, decode_split, host_experts
+    from hecate_amd import cn, router
+    from hecate_amd.cpu_tier import CpuTier, decode_split, decode_split_norm, host_experts
     lay = synth.make_layer(0, dev, resident=synth.popularity_order()[:176], shared=False)
     # the pool pinned to the CPU baseline's cores (the reference pins its workers, tier_split.py:35-36) and this
     # thread, which waits on the GPU, kept off them
@@ -238,9 +239,44 @@ def tiered_workload(torch, synth, steps, warmup, dev, threads=8):
             for i in range(32):
                 sel, _ = lay.route(xs[i])
                 cold.append(len(torch.unique(sel[sel >= 176])))
+            # the step with the post-attention norm + router and the combine into the next norm, the hand-off folded
+            # into them (norm_route posting the job, combine_norm_cpu adding the pool's partial) against the same step
+            # with the hand-off and the collect as launches of their own
+            hs = [synth.gen_normal(synth.key(synth.SEED, 0, synth.KIND["PARTIAL"], 100 + 16 * R + i), R * H, dev, 0.0,
+                                   0.5).view(R, H) for i in range(4)]
+            wp = torch.ones(H, device=dev)
+            wn = torch.ones(H, dtype=torch.bfloat16, device=dev)
+            r = torch.zeros((R, H), device=dev)
+            x2 = torch.empty((R, H), dtype=torch.bfloat16, device=dev)
+            xn = torch.empty((R, H), dtype=torch.float16, device=dev)
+            nr = torch.zeros((R, H), device=dev)
+            cand, ctr = router.norm_route_buffers(R, dev)
+
+            def fused(i):
+                r.copy_(hs[(i + 1) % 4])
+                decode_split_norm(lay, cpu, 0, hs[i % 4], r, wp, x2, wn, xn, nr, 1e-5, cand, ctr)
+
+            def launches(i):
+                r.copy_(hs[(i + 1) % 4])
+                router.norm_route(hs[i % 4], r, wp, x2, lay.wg, lay.bias, lay.sel[:R], lay.rw[:R], cand, ctr,
+                                  lay.scale, 1e-5)
+                cpu.submit(x2, lay.sel[:R], lay.rw[:R], 0)
+                lay.experts_decode(R, nr, False, xh=x2)
+                cpu.collect(nr)
+                cn.combine_norm(None, 0, nr, R, 0, 0, r, wn, xn, 1e-5)
+            # (alternating rounds, the median of each: the pool's time varies more between rounds than the launches
+            # differ)
+            ef, el_ = [], []
+            for _ in range(5):
+                ef.append(timed(torch, fused, steps, warmup))
+                el_.append(timed(torch, launches, steps, warmup))
+            el_f, el_l = float(np.median(ef)), float(np.median(el_))
+            cpu.check()
             out[f"B{R}"] = {"us_per_step": el / steps * 1e6, "us_per_token": el / steps * 1e6 / R,
                             "gpu_tier_alone_us_per_step": el_gpu / steps * 1e6,
-                            "cpu_experts_per_step_mean": float(np.mean(cold))}
+                            "cpu_experts_per_step_mean": float(np.mean(cold)),
+                            "with_norms_fused_handoff_us_per_step": el_f / steps * 1e6,
+                            "with_norms_handoff_launches_us_per_step": el_l / steps * 1e6}
     finally:
         torch.cuda.synchronize()
         cpu.close()

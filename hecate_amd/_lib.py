@@ -62,6 +62,7 @@ SIGNATURES = {
     "hmoe_cpu_stop": (i32, []),
     "hmoe_cpu_submit": (i32, [P, P, P, P, i32, i32, P]),
     "hmoe_cpu_collect": (i32, [P, P, i32, P]),
+    "hmoe_combine_norm_cpu": (i32, [P, P, P, i32, P, P, P, P, f32, f32, f32, i32, i32, P]),
     "hmoe_cpu_mailbox_alloc": (i32, [P]),
     "hmoe_cpu_mailbox_free": (i32, [P]),
 }

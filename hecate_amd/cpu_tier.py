@@ -99,6 +99,12 @@ class CpuTier:
         return out, int(self.mb.err)
 
     # ---- GPU hand-off ----
+    def handoff(self, layer):
+        """the hand-off words of router.norm_route for a job of `layer` on this pool: (mailbox, layer)"""
+        if not self.mapped:
+            raise RuntimeError("cpu tier: the hand-off needs the mapped mailbox")
+        return (self.addr, int(layer))
+
     def submit(self, x, sel, rw, layer, stream=None):
         """queue on the stream: x bf16 [R, H], sel int64 [R, 8], rw f16 [R, 8] (device) into the mailbox, flag up"""
         if not self.mapped:
@@ -185,4 +191,22 @@ def decode_split(lay, cpu, layer, x, y, with_shared=False):
     cpu.submit(x, sel, rw, layer)
     lay.experts_decode(R, y, with_shared)
     cpu.collect(y)
+    return sel, rw
+
+
+def decode_split_norm(lay, cpu, layer, h, r, w_post, x2, w_next, xn, nr, eps, cand=None, ctr=None):
+    """one decode step of a partly resident layer in the reference's fused tier form (tier_split.py:520-644 with
+    EXL3_NORM_ROUTE_HANDOFF and the combine into the next norm): norm_route adds h (fp32 [R, H], the attention output)
+    into the residual r, normalises it into x2 (bf16) with w_post, routes it into the layer's sel / rw and posts the CPU
+    tier's job in its selection launch; the resident experts run into the layer's accumulator nr (fp32 [R, H], zero on
+    entry); combine_norm_cpu then waits for the pool and adds nr + the CPU partial into r (nr zeroed), and normalises
+    it into xn with w_next (the next layer's input norm). Five launches in all, none of them for the hand-off."""
+    from . import cn, router
+    R = h.shape[0]
+    if cand is None:
+        cand, ctr = router.norm_route_buffers(R, h.device)
+    sel, rw = lay.sel[:R], lay.rw[:R]
+    router.norm_route(h, r, w_post, x2, lay.wg, lay.bias, sel, rw, cand, ctr, lay.scale, eps, ho=cpu.handoff(layer))
+    lay.experts_decode(R, nr, False, xh=x2)
+    cn.combine_norm_cpu(None, None, nr, R, cpu, r, w_next, xn, eps)
     return sel, rw

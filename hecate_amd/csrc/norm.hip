@@ -6,7 +6,7 @@
 // One 1024-thread workgroup per row, thread t owning float4 columns t and t + 1024 (t < 512), as rms_norm_kernel and
 // cn.cu:61-66 lay them out, so the 1024 chains, both butterflies and therefore r and xn are the reference's bits up
 // to the rsqrt (the reference's is fast math; here 1 / sqrt, correctly rounded).
-#include "hmoe_dev.h"
+#include "cputier_dev.h"
 
 namespace hmoe {
 
@@ -23,6 +23,8 @@ struct CnArgs
     const float* y32; const int* nparts;
     float* r; const void* w; void* xn; _Float16* xh;
     float eps, cbias, cscale;
+    hmoe_cpu_mailbox* cmb;      // CN_COMBINE: the CPU tier's mailbox (device address) whose partial is o2, or NULL
+    long long ticks;            // the bound of the wait for it
 };
 
 template <int WDT>
@@ -44,6 +46,7 @@ template <int MODE, int WDT, int XDT>
 __global__ void __launch_bounds__(1024) cn_kernel(CnArgs p)
 {
     __shared__ float gs[32];
+    __shared__ int cpu_ok;
     const int t = threadIdx.x, row = blockIdx.x;
     const size_t ro = (size_t) row * H;
     const bool hb = t + 1024 < H / 4;
@@ -51,6 +54,16 @@ __global__ void __launch_bounds__(1024) cn_kernel(CnArgs p)
     f32x4 x[2] = {z, z};
     int np = 0;
     if (MODE == CN_PARTS) np = *p.nparts;
+    // with the CPU tier: its partial is o2, once the job the norm + router posted has finished (cn.cu:114-119 waits for
+    // CPU_DONE the same way); when the wait runs out, or no job of this step was posted, nothing is added for it
+    const float* o2 = p.o2;
+    if (MODE == CN_COMBINE && p.cmb)
+    {
+        if (t == 0) cpu_ok = collect_ready(p.cmb, p.ticks);
+        __syncthreads();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
+        o2 = cpu_ok ? p.cmb->out : nullptr;
+    }
     #pragma unroll
     for (int k = 0; k < 2; ++k)
     {
@@ -63,7 +76,7 @@ __global__ void __launch_bounds__(1024) cn_kernel(CnArgs p)
             a = p.f ? *(const f32x4*) (p.f + i) : z;
             a += *(const f32x4*) (p.y + i);
             if (p.o) a += *(const f32x4*) (p.o + i);
-            if (p.o2) a += *(const f32x4*) (p.o2 + i);
+            if (o2) a += *(const f32x4*) (o2 + i);
             *(f32x4*) (p.y + i) = z;
             x[k] = a + rr;
         }
@@ -156,6 +169,28 @@ __global__ void __launch_bounds__(512) nr_logits_kernel(const uint16_t* __restri
     pair_logits<false, 2, XF16, WF16>(x2, NormIn{}, (const float*) gt, 2 * blockIdx.x, E, R, logits);
 }
 
+// the norm + router's selection with the CPU tier's hand-off folded in (nr4_kernel.cuh:360-378: the last leader writes
+// the band slot's rows and routing, then releases ISSUE): one wave per row selects as router_select_small does, then
+// the workgroup posts x2 (bf16) and the routing to the mailbox once the pool's previous job is done
+__global__ void __launch_bounds__(1024) nr_select_post_kernel(const float* __restrict__ logits,
+    const float* __restrict__ bias, int R, int E, int topk, float scale, int64_t* __restrict__ sel,
+    uint16_t* __restrict__ rw, const uint16_t* __restrict__ x2, hmoe_cpu_mailbox* mb, int layer, long long ticks)
+{
+    __shared__ int ready;
+    __shared__ uint32_t gen;
+    if (threadIdx.x == 0) {
+        uint32_t g;
+        ready = post_begin(mb, ticks, g);
+        gen = g;
+    }
+    const int r = threadIdx.x >> 6;
+    if (r < R) select_row(logits + (size_t) r * RMAXE, bias, E, topk, scale, sel + (size_t) r * topk, rw + (size_t) r * topk);
+    // (the rows' selections, stored by their waves, are seen by the whole workgroup past the barrier)
+    __syncthreads();
+    if (!ready) return;
+    post_job(mb, (const uint4*) x2, (const uint4*) sel, (const uint4*) rw, R, layer, gen, 1024);
+}
+
 }  // namespace hmoe
 
 using namespace hmoe;
@@ -169,7 +204,22 @@ extern "C" int hmoe_combine_norm(const float* f, const float* o, float* y, int r
     HMOE_REQUIRE(!done, "combine_norm: the cross-device DONE flag is not supported (the RTX band is not built)");
     HMOE_REQUIRE(((uintptr_t) f & 15) == 0 && ((uintptr_t) y & 15) == 0 && ((uintptr_t) o & 15) == 0 &&
                  ((uintptr_t) o2 & 15) == 0, "combine_norm: alignment");
-    CnArgs a = {f, o, y, o2, nullptr, nullptr, r, w, xn, nullptr, eps, cbias, cscale};
+    CnArgs a = {f, o, y, o2, nullptr, nullptr, r, w, xn, nullptr, eps, cbias, cscale, nullptr, 0};
+    return launch_cn<CN_COMBINE>(a, rows, w_dtype, xn_dtype, (hipStream_t) stream);
+}
+
+extern "C" int hmoe_combine_norm_cpu(const float* f, const float* o, float* y, int rows, hmoe_cpu_mailbox* mb,
+                                     float* r, const void* w, void* xn, float eps, float cbias, float cscale,
+                                     int w_dtype, int xn_dtype, void* stream)
+{
+    if (int rc = check_norm("combine_norm_cpu", r, w, xn, rows, HMOE_CPU_MAXR, w_dtype, xn_dtype)) return rc;
+    HMOE_REQUIRE(y && mb, "combine_norm_cpu: null y or mailbox");
+    HMOE_REQUIRE(((uintptr_t) f & 15) == 0 && ((uintptr_t) y & 15) == 0 && ((uintptr_t) o & 15) == 0,
+                 "combine_norm_cpu: alignment");
+    hmoe_cpu_mailbox* d = nullptr;
+    long long ticks = 0;
+    if (int rc = cpu_mailbox_device(mb, &d, &ticks)) return rc;
+    CnArgs a = {f, o, y, nullptr, nullptr, nullptr, r, w, xn, nullptr, eps, cbias, cscale, d, ticks};
     return launch_cn<CN_COMBINE>(a, rows, w_dtype, xn_dtype, (hipStream_t) stream);
 }
 
@@ -178,7 +228,7 @@ extern "C" int hmoe_residual_rmsnorm(float* r, float* a, const float* w, int R, 
 {
     if (int rc = check_norm("residual_rmsnorm", r, w, xn, R, 1 << 20, HMOE_DT_F32, HMOE_DT_BF16)) return rc;
     HMOE_REQUIRE(((uintptr_t) a & 15) == 0 && ((uintptr_t) xh & 7) == 0, "residual_rmsnorm: alignment");
-    CnArgs c = {nullptr, nullptr, a, nullptr, nullptr, nullptr, r, w, xn, (_Float16*) xh, eps, 0.f, 1.f};
+    CnArgs c = {nullptr, nullptr, a, nullptr, nullptr, nullptr, r, w, xn, (_Float16*) xh, eps, 0.f, 1.f, nullptr, 0};
     return launch_cn<CN_ADD>(c, R, HMOE_DT_F32, HMOE_DT_BF16, (hipStream_t) stream);
 }
 
@@ -205,7 +255,6 @@ extern "C" int hmoe_norm_route(const float* y, float* r, const void* w, void* x2
                                int gt_dtype, void* stream)
 {
     (void) ctr;
-    (void) ho;
     if (int rc = check_norm("norm_route", r, w, x2, R, MAXR, w_dtype, x2_dtype)) return rc;
     HMOE_REQUIRE(y && gt && sel && rw && cand, "norm_route: null buffer");
     HMOE_REQUIRE(E >= TOPK && E <= RMAXE, "norm_route: %d experts", E);
@@ -213,8 +262,21 @@ extern "C" int hmoe_norm_route(const float* y, float* r, const void* w, void* x2
                  gt_dtype);
     HMOE_REQUIRE(((uintptr_t) y & 15) == 0 && ((uintptr_t) gt & 15) == 0 && ((uintptr_t) x2 & 15) == 0,
                  "norm_route: alignment");
-    HMOE_REQUIRE(n_ho == 0, "norm_route: the band hand-off (ho) is not supported here; post the CPU tier's job with "
-                 "hmoe_cpu_submit after the routing");
+    // the hand-off: none, or this build's CPU tier {mailbox, layer} (the reference's 10 / 11 words address its RTX and
+    // Grace bands' slots, which are not built here)
+    HMOE_REQUIRE(n_ho == 0 || (n_ho == 2 && ho), "norm_route: the hand-off ho must be empty or {mailbox, layer} (%d words)", n_ho);
+    hmoe_cpu_mailbox* mb = nullptr;
+    long long ticks = 0;
+    int layer = 0;
+    if (n_ho == 2)
+    {
+        HMOE_REQUIRE(ho[0] != 0 && ho[1] >= 0 && ho[1] <= INT32_MAX, "norm_route: hand-off mailbox / layer");
+        HMOE_REQUIRE(x2_dtype == HMOE_DT_BF16 && R <= HMOE_CPU_MAXR, "norm_route: the CPU tier's hand-off takes bf16 x2 "
+                     "and at most %d rows (%d)", HMOE_CPU_MAXR, R);
+        HMOE_REQUIRE((((uintptr_t) sel | (uintptr_t) rw) & 15) == 0, "norm_route: sel / rw not 16-byte aligned");
+        if (int rc = cpu_mailbox_device((hmoe_cpu_mailbox*) (uintptr_t) ho[0], &mb, &ticks)) return rc;
+        layer = (int) ho[1];
+    }
     hipStream_t st = (hipStream_t) stream;
     CnArgs a = {nullptr, nullptr, (float*) y, nullptr, nullptr, nullptr, r, w, x2, nullptr, eps, cbias, cscale};
     if (int rc = launch_cn<CN_ROUTE>(a, R, w_dtype, x2_dtype, st)) return rc;
@@ -225,5 +287,8 @@ extern "C" int hmoe_norm_route(const float* y, float* r, const void* w, void* x2
     else if (wf16) nr_logits_kernel<false, true><<<g, 512, 0, st>>>((const uint16_t*) x2, gt, cand, R, E);
     else nr_logits_kernel<false, false><<<g, 512, 0, st>>>((const uint16_t*) x2, gt, cand, R, E);
     if (int rc = HMOE_LAUNCHED("norm_route logits")) return rc;
-    return router_select_small(cand, bias, R, E, TOPK, scale, sel, rw, st);
+    if (!mb) return router_select_small(cand, bias, R, E, TOPK, scale, sel, rw, st);
+    nr_select_post_kernel<<<1, 1024, 0, st>>>(cand, bias, R, E, TOPK, scale, sel, rw, (const uint16_t*) x2, mb, layer,
+                                              ticks);
+    return HMOE_LAUNCHED("norm_route select + hand-off");
 }

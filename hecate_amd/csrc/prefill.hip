@@ -683,10 +683,10 @@ extern "C" int hmoe_shared_forward(const void* x, int T, const void* sh_gw, cons
     if (T == 0) return HMOE_OK;
     HMOE_REQUIRE(x && sh_gw && sh_uw && sh_dw && work && out && T > 0, "shared_forward: arguments");
     HMOE_REQUIRE(xf == HMOE_XF_BF16 || xf == HMOE_XF_F16, "shared_forward: xf must be HMOE_XF_BF16 (0) or HMOE_XF_F16 (2)");
-    HMOE_REQUIRE(((uintptr_t) x & 15) == 0 && ((uintptr_t) work & 255) == 0 && ((uintptr_t) out & 15) == 0,
-                 "shared_forward: alignment (x, out 16 bytes, work 256)");
     // (the dense GEMMs address their input rows by 32-bit byte offsets)
     HMOE_REQUIRE((size_t) T * H * 2 <= UINT32_MAX, "shared_forward: T %d past the 4 GB input offsets", T);
+    HMOE_REQUIRE(((uintptr_t) x & 15) == 0 && ((uintptr_t) work & 255) == 0 && ((uintptr_t) out & 15) == 0,
+                 "shared_forward: alignment (x, out 16 bytes, work 256)");
     hipStream_t st = (hipStream_t) stream;
     uint8_t* wk = (uint8_t*) work;
     const _Float16* xs = (const _Float16*) x;

@@ -3,6 +3,8 @@
 router_fused(x, wt, bias, logits, ctr, sel, rw, topk, scale) keeps the reference's arguments (x bf16 here, wt fp32
 [E, K]); the trailing xh receives an f16 copy of x (moe4.forward reads fp16 x as the reference does). Any row count (the reference handles 2..8).
 """
+import ctypes
+
 import torch
 
 from ._lib import call, dt_of, lib, on_device, ptr, stream_of
@@ -55,19 +57,23 @@ def norm_route_buffers(R, device, E=256):
 def norm_route(y, r, w, x2, gt, bias, sel, rw, cand, ctr, scale, eps, cbias=0.0, cscale=1.0, ho=None):
     """runtime/core/exl3_normroute.py:16-65 norm_route (nr4_kernel.cuh:122-381): r = y + r, x2 = RMSNorm(r) * (w +
     cbias) * cscale (fp16 as in the reference, or bf16), then the router on x2: gt [E, H] fp16 (the reference's
-    transposed gate) or fp32, bias fp32 [E] or None, sel int64 / rw fp16 [R, 8]. cand / ctr: norm_route_buffers. ho
-    (the reference's band hand-off words) must be empty: post the CPU tier's job with CpuTier after the routing."""
+    transposed gate) or fp32, bias fp32 [E] or None, sel int64 / rw fp16 [R, 8]. cand / ctr: norm_route_buffers. ho:
+    the band hand-off words, empty or (mailbox, layer) of this build's CPU tier (CpuTier.handoff(layer)): the
+    selection launch then also posts the CPU tier's job (x2 bf16, R <= 8), as the reference's kernel releases its
+    Grace band's ISSUE (nr4_kernel.cuh:360-378); the reference's 10 / 11-word form addresses bands not built here."""
     on_device("norm_route", y, r, w, x2, gt, bias, sel, rw, cand, ctr)
     R = y.numel() // y.shape[-1]
     E = gt.shape[0]
-    if ho:
-        raise RuntimeError("norm_route: the band hand-off (ho) is not supported; post the CPU tier's job after routing")
+    ho = list(ho) if ho else []
+    if ho and len(ho) != 2:
+        raise RuntimeError("norm_route: ho must be empty or (mailbox, layer)")
+    hw = (ctypes.c_int64 * 2)(*[int(v) for v in ho]) if ho else None
     if not (y.dtype == torch.float32 and r.dtype == torch.float32 and y.shape[-1] == 6144 and r.numel() == y.numel()
             and x2.numel() >= y.numel() and y.is_contiguous() and r.is_contiguous() and x2.is_contiguous()
             and gt.is_contiguous() and gt.shape[1] == 6144 and w.numel() == 6144 and sel.dtype == torch.int64
             and rw.dtype == torch.float16 and cand.numel() * 4 >= int(lib().hmoe_norm_route_scratch_bytes(R, E))):
         raise RuntimeError("norm_route: shape / dtype")
     call("hmoe_norm_route", ptr(y), ptr(r), ptr(w), ptr(x2), ptr(gt), ptr(bias), ptr(sel), ptr(rw), ptr(cand),
-         ptr(ctr), float(scale), float(eps), float(cbias), float(cscale), None, 0, int(R), int(E), dt_of(w),
+         ptr(ctr), float(scale), float(eps), float(cbias), float(cscale), ctypes.addressof(hw) if hw else None, len(ho), int(R), int(E), dt_of(w),
          dt_of(x2, ("bfloat16", "float16")), dt_of(gt, ("float32", "float16")), stream_of(y.device))
     return sel, rw

@@ -259,10 +259,14 @@ int hmoe_combine_norm(const float* f, const float* o, float* y, int rows, const 
  * fp32 or the reference's f16, gt_dtype) in router_fused's fixed order, sel int64 / rw f16 [R][8] by router_fused's
  * rules (sigmoid + bias keys, ties to the lowest index, rw = f16(a * scale / (sum a + 1e-20))). cand: logits scratch of
  * hmoe_norm_route_scratch_bytes(R, E) bytes (the reference's candidate buffer has the same role); ctr unused (kept for
- * the argument position). ho: the reference's band hand-off words; n_ho must be 0 (the CPU tier's job is posted by
- * hmoe_cpu_submit after the routing). R in [1, 16] (the reference: 2..8), E in [8, 256]. Three launches: the norm
- * (one workgroup per row), the logits (two experts per workgroup), the selection; r and x2 are those of
- * hmoe_combine_norm's norm, the routing that of hmoe_router_fused on x2. */
+ * the argument position). ho (n_ho words, host memory): the band hand-off. The reference's 10 / 11 words address its RTX
+ * and Grace bands' slots and flags (exl3_normroute.py:38-47), which this build does not have; here n_ho is 0 (no
+ * hand-off) or 2, {mailbox, layer}: the selection launch also posts the CPU tier's job as hmoe_cpu_submit does (waits
+ * for the pool's previous job, copies x2 and the routing into the mailbox, releases issue), which nr4_kernel.cuh:
+ * 360-378 does for the reference's Grace band; it needs bf16 x2, R <= HMOE_CPU_MAXR and 16-byte aligned sel / rw.
+ * R in [1, 16] (the reference: 2..8), E in [8, 256]. Three launches: the norm (one workgroup per row), the logits (two
+ * experts per workgroup), the selection (with the post); r and x2 are those of hmoe_combine_norm's norm, the routing
+ * that of hmoe_router_fused on x2. */
 size_t hmoe_norm_route_scratch_bytes(int R, int E);
 int hmoe_norm_route(const float* y, float* r, const void* w, void* x2, const void* gt, const float* bias, int64_t* sel,
                     uint16_t* rw, float* cand, int* ctr, float scale, float eps, float cbias, float cscale,
@@ -341,6 +345,15 @@ int hmoe_cpu_stop(void);
 int hmoe_cpu_submit(hmoe_cpu_mailbox* mb, const void* x, const int64_t* sel, const uint16_t* rw, int R, int layer,
                     void* stream);
 int hmoe_cpu_collect(hmoe_cpu_mailbox* mb, float* y, int R, void* stream);
+/* runtime/tier/cn.cu:108-142 combine_norm_pdl's CPU_DONE form for this build's CPU tier: hmoe_combine_norm with the
+ * pool's partial (the mailbox's out) in the o2 position, added once the job the last post (hmoe_norm_route with a
+ * hand-off, or hmoe_cpu_submit) issued has finished: a = ((f + y) + o) + out, y zeroed, r = a + r, xn = RMSNorm(r).
+ * The wait is bounded as hmoe_cpu_collect's; past it, or with gpu_err already set, out is not added and gpu_err says
+ * so. rows in [1, HMOE_CPU_MAXR] (the job's rows). With the post folded into the norm + router and the collect into
+ * this combine, a tiered layer needs no launch of its own for the hand-off. */
+int hmoe_combine_norm_cpu(const float* f, const float* o, float* y, int rows, hmoe_cpu_mailbox* mb, float* r,
+                          const void* w, void* xn, float eps, float cbias, float cscale, int w_dtype, int xn_dtype,
+                          void* stream);
 /* a mapped, coherent pinned mailbox (hipHostMalloc) and its release */
 int hmoe_cpu_mailbox_alloc(hmoe_cpu_mailbox** mb);
 int hmoe_cpu_mailbox_free(hmoe_cpu_mailbox* mb);

@@ -314,13 +314,35 @@ def test_norm_entries_refuse_bad_arguments():
     assert L.hmoe_norm_route(A, A, A, A, A, None, A, A, None, A, 2.5, 1e-5, 0.0, 1.0, None, 0, 4, 256, F16, F16, F16,
                              None) != 0
     assert L.hmoe_norm_route_scratch_bytes(8, 256) == 8 * 256 * 4
+    # the CPU tier's hand-off {mailbox, layer}: bf16 x2, at most 8 rows, a mailbox, 16-byte aligned sel / rw
+    ho2 = (ctypes.c_int64 * 2)(A, 3)
+    assert L.hmoe_norm_route(A, A, A, A, A, None, A, A, A, A, 2.5, 1e-5, 0.0, 1.0, ho2, 2, 4, 256, F16, F16, F16,
+                             None) != 0
+    assert b"bf16" in L.hmoe_last_error()
+    assert L.hmoe_norm_route(A, A, A, A, A, None, A, A, A, A, 2.5, 1e-5, 0.0, 1.0, ho2, 2, 9, 256, F16, BF16, F16,
+                             None) != 0
+    assert L.hmoe_norm_route(A, A, A, A, A, None, A + 8, A, A, A, 2.5, 1e-5, 0.0, 1.0, ho2, 2, 4, 256, F16, BF16, F16,
+                             None) != 0
+    assert b"aligned" in L.hmoe_last_error()
+    assert L.hmoe_norm_route(A, A, A, A, A, None, A, A, A, A, 2.5, 1e-5, 0.0, 1.0, (ctypes.c_int64 * 2)(0, 3), 2, 4,
+                             256, F16, BF16, F16, None) != 0
+    assert b"mailbox" in L.hmoe_last_error()
+    assert L.hmoe_norm_route(A, A, A, A, A, None, A, A, A, A, 2.5, 1e-5, 0.0, 1.0, None, 2, 4, 256, F16, BF16, F16,
+                             None) != 0
+    # combine_norm_cpu(f, o, y, rows, mb, r, w, xn, eps, cbias, cscale, wdt, xdt, st)
+    assert L.hmoe_combine_norm_cpu(None, None, A, 9, A, A, A, A, 1e-5, 0.0, 1.0, F16, F16, None) != 0
+    assert b"rows" in L.hmoe_last_error()
+    assert L.hmoe_combine_norm_cpu(None, None, A, 4, None, A, A, A, 1e-5, 0.0, 1.0, F16, F16, None) != 0
+    assert b"mailbox" in L.hmoe_last_error()
+    assert L.hmoe_combine_norm_cpu(None, None, A + 4, 4, A, A, A, A, 1e-5, 0.0, 1.0, F16, F16, None) != 0
+    assert b"alignment" in L.hmoe_last_error()
     # decode_combine_norm(y32, ctr, R, r, w, xn, xh, eps, cbias, cscale, wdt, xdt, st)
     assert L.hmoe_decode_combine_norm(None, A, 4, A, A, A, None, 1e-5, 0.0, 1.0, F32, BF16, None) != 0
     assert L.hmoe_decode_combine_norm(A, A, 17, A, A, A, None, 1e-5, 0.0, 1.0, F32, BF16, None) != 0
 
 
 def test_norm_mirrors_check_before_calling():
-    """the Python mirrors refuse host tensors, a non-empty hand-off and wrong dtypes before calling the library"""
+    """the Python mirrors refuse host tensors and wrong dtypes before calling the library"""
     import torch
     from hecate_amd import cn, router
     y = torch.zeros(2, 6144)
@@ -331,6 +353,9 @@ def test_norm_mirrors_check_before_calling():
         router.norm_route(y, y, torch.zeros(6144), torch.zeros(2, 6144, dtype=torch.float16), torch.zeros(256, 6144),
                           None, torch.zeros(2, 8, dtype=torch.int64), torch.zeros(2, 8, dtype=torch.float16),
                           torch.zeros(2048), torch.zeros(64, dtype=torch.int32), 2.5, 1e-5)
+    with pytest.raises(RuntimeError, match="device"):
+        cn.combine_norm_cpu(None, 0, y, 2, 1 << 20, y, torch.zeros(6144, dtype=torch.float16),
+                            torch.zeros(2, 6144, dtype=torch.float16), 1e-5)
     with pytest.raises(RuntimeError, match="dtype"):
         _lib.dt_of(torch.zeros(1, dtype=torch.int32))
     assert _lib.dt_of(torch.zeros(1, dtype=torch.float16)) == 2 and _lib.dt_of(torch.zeros(1)) == 0

@@ -114,3 +114,114 @@ def test_tiered_split_replays_in_a_graph(dev, split):
         cpu.check()
         assert torch.equal(y2, refs[(i + 1) % 3]), i
     assert cpu.stats()[0] == j0 + 6
+
+
+def _norm_inputs(R, dev, seed):
+    g = torch.Generator().manual_seed(seed)
+    h = (torch.randn((R, H), generator=g) * 0.5).to(dev)
+    r0 = (torch.randn((R, H), generator=g) * 2.0).to(dev)
+    w_post = (1.0 + 0.02 * torch.randn(H, generator=g)).to(dev)
+    w_next = (1.0 + 0.02 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev)
+    return h, r0, w_post, w_next
+
+
+def _launch_form(lay, cpu, h, r, w_post, w_next, x2, xn, nr, eps):
+    """the same step with the hand-off and the collect as launches of their own: norm_route, cpu submit, the resident
+    experts, cpu collect into nr, combine_norm of nr"""
+    from hecate_amd import cn, router
+    R = h.shape[0]
+    cand, ctr = router.norm_route_buffers(R, h.device)
+    router.norm_route(h, r, w_post, x2, lay.wg, lay.bias, lay.sel[:R], lay.rw[:R], cand, ctr, lay.scale, eps)
+    cpu.submit(x2, lay.sel[:R], lay.rw[:R], 0)
+    lay.experts_decode(R, nr, False, xh=x2)
+    cpu.collect(nr)
+    cn.combine_norm(None, 0, nr, R, 0, 0, r, w_next, xn, eps)
+
+
+@pytest.mark.parametrize("R", [1, 4, 8])
+def test_tiered_fused_handoff_matches_the_launch_form(dev, split, R):
+    """norm_route posting the CPU tier's job in its selection launch and combine_norm_cpu adding the pool's partial
+    once the job is done (the reference's nr4 hand-off and cn CPU_DONE form) give the bits of the same step with the
+    hand-off and the collect as launches of their own: x2, the routing, r and the next layer's xn; one pool job per
+    step, the accumulator left zeroed"""
+    from hecate_amd.cpu_tier import decode_split_norm
+    log(f"fused hand-off R={R}")
+    s = split
+    lay, cpu = s["lay"], s["cpu"]
+    h, r0, w_post, w_next = _norm_inputs(R, dev, 60 + R)
+    eps = 1e-5
+    outs = []
+    for fused in (True, False):
+        r = r0.clone()
+        x2 = torch.empty((R, H), dtype=torch.bfloat16, device=dev)
+        xn = torch.empty((R, H), dtype=torch.float16, device=dev)
+        nr = torch.zeros((R, H), dtype=torch.float32, device=dev)
+        jobs0 = cpu.stats()[0]
+        if fused:
+            decode_split_norm(lay, cpu, 0, h, r, w_post, x2, w_next, xn, nr, eps)
+        else:
+            _launch_form(lay, cpu, h, r, w_post, w_next, x2, xn, nr, eps)
+        torch.cuda.synchronize()
+        cpu.check()
+        assert cpu.stats()[0] == jobs0 + 1
+        assert not bool(nr.any())
+        outs.append((x2.view(torch.int16).clone(), lay.sel[:R].clone(), lay.rw[:R].view(torch.int16).clone(),
+                     r.view(torch.int32).clone(), xn.view(torch.int16).clone()))
+    log(f"  cold picks {int((outs[0][1] >= N_RES).sum())} of {outs[0][1].numel()}")
+    for name, a, b in zip(("x2", "sel", "rw", "r", "xn"), outs[0], outs[1]):
+        assert torch.equal(a, b), name
+
+
+def test_tiered_fused_handoff_replays_in_a_graph(dev, split):
+    """the fused step (norm_route with the hand-off, the resident experts, combine_norm_cpu) captured in a hipGraph:
+    each replay, on new inputs, runs one CPU job and gives the eager bits; eager steps run between the replays"""
+    from hecate_amd.cpu_tier import decode_split_norm
+    s = split
+    lay, cpu = s["lay"], s["cpu"]
+    R, eps = 4, 1e-5
+    ins = [_norm_inputs(R, dev, 80 + i) for i in range(4)]
+    w_post, w_next = ins[0][2], ins[0][3]
+
+    def eager(i):
+        h, r0 = ins[i][0], ins[i][1]
+        r = r0.clone()
+        x2 = torch.empty((R, H), dtype=torch.bfloat16, device=dev)
+        xn = torch.empty((R, H), dtype=torch.float16, device=dev)
+        nr = torch.zeros((R, H), dtype=torch.float32, device=dev)
+        decode_split_norm(lay, cpu, 0, h, r, w_post, x2, w_next, xn, nr, eps)
+        torch.cuda.synchronize()
+        cpu.check()
+        return r.clone(), xn.clone()
+
+    refs = [eager(i) for i in range(3)]
+    assert not torch.equal(refs[0][1], refs[1][1])
+    from hecate_amd import router
+    hg, rg, r0g = ins[3][0].clone(), ins[3][1].clone(), ins[3][1].clone()
+    x2g = torch.empty((R, H), dtype=torch.bfloat16, device=dev)
+    xng = torch.empty((R, H), dtype=torch.float16, device=dev)
+    nrg = torch.zeros((R, H), dtype=torch.float32, device=dev)
+    cand, ctr = router.norm_route_buffers(R, dev)
+    st = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(st):
+        rg.copy_(r0g)
+        decode_split_norm(lay, cpu, 0, hg, rg, w_post, x2g, w_next, xng, nrg, eps, cand, ctr)
+        torch.cuda.synchronize()
+        cpu.check()
+        with torch.cuda.graph(g, stream=st):
+            rg.copy_(r0g)
+            decode_split_norm(lay, cpu, 0, hg, rg, w_post, x2g, w_next, xng, nrg, eps, cand, ctr)
+    torch.cuda.synchronize()
+    cpu.check()
+    j0 = cpu.stats()[0]
+    for i in range(3):
+        hg.copy_(ins[i][0])
+        r0g.copy_(ins[i][1])
+        g.replay()
+        torch.cuda.synchronize()
+        cpu.check()
+        assert torch.equal(rg, refs[i][0]) and torch.equal(xng, refs[i][1]), i
+        assert not bool(nrg.any())
+        r2, xn2 = eager((i + 1) % 3)
+        assert torch.equal(r2, refs[(i + 1) % 3][0]) and torch.equal(xn2, refs[(i + 1) % 3][1]), i
+    assert cpu.stats()[0] == j0 + 6
