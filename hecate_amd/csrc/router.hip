@@ -5,8 +5,8 @@
 //   small (R <= 16): a logits kernel (two experts per workgroup, one 32-element chunk per thread, chunk sums folded
 //                    through LDS) and a select kernel (one wave per row); the kernel boundary replaces the reference's
 //                    last-block counter (exl3_router.py:74-83,130), whose cross-workgroup fences are costly on gfx950.
-//   large (R > 16) : a register-tiled fp32 GEMM per (128 rows, 128 experts, segment) with the same chain order, then a
-//                    select kernel that folds the 8 segment sums and picks each row's top-k (one wave per row).
+//   large (R > 16) : an fp32 MFMA GEMM per (128 rows, 64 experts, segment) with the same chain order, then a select
+//                    kernel that folds the 8 segment sums and picks each row's top-k (one wave per row).
 #include "hmoe_dev.h"
 
 namespace hmoe {
@@ -50,26 +50,25 @@ __global__ void __launch_bounds__(1024) router_select_small_kernel(const float* 
     select_row(logits + (size_t) r * RMAXE, bias, E, topk, scale, sel + (size_t) r * topk, rw + (size_t) r * topk);
 }
 
-// large path, 1: segment sums seg[s][r][e] for a 128-row x 16 TE-expert tile of one segment, 8 x TE outputs per
-// thread (thread (ty, tx) of 16 x 16: rows 8 ty .., experts TE tx ..). A 32-k chunk of x (bf16 -> fp32) and of w is staged in
-// LDS k-major, so a thread reads its 8 rows and its 8 experts of one k as two 32-byte runs; the next chunk's global
-// loads are in flight while this chunk computes (two LDS buffers, one barrier per chunk). Per output: per chunk a
-// fmaf chain over k ascending from 0, the chunk totals added in order from 0 (the order of the small path).
-constexpr int SG_R = 128;
-template <int TE>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) router_seg_kernel(
+// large path, 1: the segment sums seg[s][r][e] on the matrix cores. v_mfma_f32_16x16x4f32 computes each output as a
+// fmaf chain over its 4 k in order from the accumulator (measured bit-equal to that chain on every output of
+// random, signed-zero and denormal operands), so a chunk's 32-element chain is 8 MFMAs from a zero accumulator, in the
+// order of the small path and the oracle. Workgroup = 128 rows x 64 experts of one segment, 4 waves; wave w owns rows
+// 32 w .. + 32 (2 row tiles) x the 64 experts (4 tiles): per 4-k step lane l reads A = x[row l % 16][k l / 16] and
+// B = w[expert l % 16][k l / 16] from the k-major LDS chunk and holds D rows 4 (l / 16) .. + 4 of expert l % 16.
+// A 32-k chunk of x (bf16 -> fp32) and of w is staged in LDS k-major (rows padded by 4 floats); the next chunk's
+// global loads are in flight while this chunk computes (two buffers, one barrier per chunk).
+constexpr int SM_R = 128, SM_E = 64, SM_XP = SM_R + 4, SM_WP = SM_E + 4;
+__global__ void __launch_bounds__(256) router_seg_mfma_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ wt, float* __restrict__ seg, int R, int K, int E)
 {
-    constexpr int SG_E = 16 * TE, WJ = 4 * TE / 8;      // experts per tile; w loads per thread per chunk
-    static_assert(TE == 4 || TE == 8, "4 or 8 experts per thread");
-    __shared__ __attribute__((aligned(16))) float xs[2][RCHUNK][SG_R];
-    __shared__ __attribute__((aligned(16))) float ws[2][RCHUNK][SG_E];
-    const int r0 = blockIdx.x * SG_R, e0 = blockIdx.y * SG_E, s = blockIdx.z;
-    const int t = threadIdx.x, ty = t >> 4, tx = t & 15;
+    constexpr int WJ = 2;                                       // w loads (4 floats) per thread per chunk
+    __shared__ __attribute__((aligned(16))) float xs[2][RCHUNK][SM_XP];
+    __shared__ __attribute__((aligned(16))) float ws[2][RCHUNK][SM_WP];
+    const int r0 = blockIdx.x * SM_R, e0 = blockIdx.y * SM_E, s = blockIdx.z;
+    const int t = threadIdx.x, l = t & 63, w = t >> 6;
     const int segk = K / RSEG, k0 = s * segk, nch = segk / RCHUNK;
-    // staging: thread t loads row t % 128 of the tile, k 8 h .. + 8 for h = t / 128 and h + 2, and expert t % SG_E,
-    // k 4 h .. + 4 for h = t / SG_E + (256 / SG_E) j, j < WJ (rows / experts past the end load row 0 and stage zeros)
-    const int sr = t & 127, sh = t >> 7, se = t % SG_E, seh = t / SG_E;
+    const int sr = t & 127, sh = t >> 7, se = t % SM_E, seh = t / SM_E;
     const bool xin = r0 + sr < R, win = e0 + se < E;
     const uint16_t* xp = x + (size_t) (xin ? r0 + sr : 0) * K + k0;
     const float* wp = wt + (size_t) (win ? e0 + se : 0) * K + k0;
@@ -79,7 +78,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) r
         #pragma unroll
         for (int h = 0; h < 2; ++h) gx[h] = *(const u32x4*) (xp + c * RCHUNK + 8 * (sh + 2 * h));
         #pragma unroll
-        for (int j = 0; j < WJ; ++j) gw[j] = *(const f32x4*) (wp + c * RCHUNK + 4 * (seh + (256 / SG_E) * j));
+        for (int j = 0; j < WJ; ++j) gw[j] = *(const f32x4*) (wp + c * RCHUNK + 4 * (seh + 4 * j));
     };
     auto store = [&](int b) {
         #pragma unroll
@@ -94,61 +93,60 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) r
         #pragma unroll
         for (int j = 0; j < WJ; ++j)
             #pragma unroll
-            for (int q = 0; q < 4; ++q) ws[b][4 * (seh + (256 / SG_E) * j) + q][se] = win ? gw[j][q] : 0.f;
+            for (int q = 0; q < 4; ++q) ws[b][4 * (seh + 4 * j) + q][se] = win ? gw[j][q] : 0.f;
     };
-    float acc[8][TE], tot[8][TE];
+    f32x4 tot[2][4];
     #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 2; ++i)
         #pragma unroll
-        for (int j = 0; j < TE; ++j) tot[i][j] = 0.f;
+        for (int j = 0; j < 4; ++j) tot[i][j] = (f32x4) {0.f, 0.f, 0.f, 0.f};
     load(0);
     store(0);
     __syncthreads();
+    const int ar = 32 * w + (l & 15), kl = l >> 4;
     for (int c = 0; c < nch; ++c)
     {
         const int b = c & 1;
         if (c + 1 < nch) load(c + 1);
+        f32x4 d[2][4];
         #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            #pragma unroll
-            for (int j = 0; j < TE; ++j) acc[i][j] = 0.f;
-        #pragma unroll 4
-        for (int k = 0; k < RCHUNK; ++k)
+        for (int kk = 0; kk < RCHUNK / 4; ++kk)
         {
-            const f32x4 xa = *(const f32x4*) &xs[b][k][8 * ty], xb = *(const f32x4*) &xs[b][k][8 * ty + 4];
-            float xv[8] = {xa[0], xa[1], xa[2], xa[3], xb[0], xb[1], xb[2], xb[3]}, wv[TE];
+            const int k = 4 * kk + kl;
+            float a[2], bv[4];
             #pragma unroll
-            for (int j = 0; j < TE; j += 4)
-            {
-                const f32x4 wq = *(const f32x4*) &ws[b][k][TE * tx + j];
-                #pragma unroll
-                for (int q = 0; q < 4; ++q) wv[j + q] = wq[q];
-            }
+            for (int i = 0; i < 2; ++i) a[i] = xs[b][k][ar + 16 * i];
             #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int j = 0; j < 4; ++j) bv[j] = ws[b][k][16 * j + (l & 15)];
+            #pragma unroll
+            for (int i = 0; i < 2; ++i)
                 #pragma unroll
-                for (int j = 0; j < TE; ++j) acc[i][j] = __builtin_fmaf(xv[i], wv[j], acc[i][j]);
+                for (int j = 0; j < 4; ++j)
+                    d[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], bv[j],
+                                                                   kk == 0 ? (f32x4) {0.f, 0.f, 0.f, 0.f} : d[i][j],
+                                                                   0, 0, 0);
         }
         #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < 2; ++i)
             #pragma unroll
-            for (int j = 0; j < TE; ++j) tot[i][j] = tot[i][j] + acc[i][j];
-        // the other buffer was last read in the previous chunk, before the barrier that ended it
+            for (int j = 0; j < 4; ++j) tot[i][j] = tot[i][j] + d[i][j];
         if (c + 1 < nch) store(b ^ 1);
         __syncthreads();
     }
     #pragma unroll
-    for (int i = 0; i < 8; ++i)
-    {
-        const int r = r0 + 8 * ty + i;
-        if (r >= R) break;
+    for (int i = 0; i < 2; ++i)
         #pragma unroll
-        for (int j = 0; j < TE; ++j)
+        for (int q = 0; q < 4; ++q)
         {
-            const int e = e0 + TE * tx + j;
-            if (e < E) seg[((size_t) s * R + r) * RMAXE + e] = tot[i][j];
+            const int r = r0 + 32 * w + 16 * i + 4 * (l >> 4) + q;
+            if (r >= R) continue;
+            #pragma unroll
+            for (int j = 0; j < 4; ++j)
+            {
+                const int e = e0 + 16 * j + (l & 15);
+                if (e < E) seg[((size_t) s * R + r) * RMAXE + e] = tot[i][j][q];
+            }
         }
-    }
 }
 
 // large path, 2: fold the segments in order, select; one wave per row; optional f16 copy of x
@@ -219,11 +217,7 @@ extern "C" int hmoe_router_fused(const void* x, const float* wt, const float* bi
     }
     // 128 experts per workgroup from 4096 rows (the 8 x 8 tiles are faster at 8192 rows, -115 us); fewer rows take 64
     // experts per workgroup, so that the grid still fills the CUs twice over
-    if (R >= 4096)
-        router_seg_kernel<8><<<dim3((R + SG_R - 1) / SG_R, (E + 127) / 128, RSEG), 256, 0, st>>>(
-            (const uint16_t*) x, wt, logits, R, K, E);
-    else
-        router_seg_kernel<4><<<dim3((R + SG_R - 1) / SG_R, (E + 63) / 64, RSEG), 256, 0, st>>>(
+    router_seg_mfma_kernel<<<dim3((R + SM_R - 1) / SM_R, (E + SM_E - 1) / SM_E, RSEG), 256, 0, st>>>(
             (const uint16_t*) x, wt, logits, R, K, E);
     router_select_kernel<<<(R + 3) / 4, 256, 0, st>>>(logits, bias, R, E, topk, scale, sel, rw, (const uint16_t*) x,
                                                       (_Float16*) xh, K);

@@ -88,15 +88,31 @@ def test_router_bit_exact(dev, R, bias_sigma):
     assert np.array_equal(u16(xh), O.f32_to_f16(O.bf16_to_f32(x)))
 
 
-@pytest.mark.parametrize("R,E", [(300, 160), (4100, 200)])
-def test_router_large_path_partial_tiles(dev, R, E):
-    """the large path's segment GEMM on partial tiles: 300 rows (128-row tiles, 64 experts per workgroup) and 4100 rows
-    (128 experts per workgroup) with fewer experts than a whole tile covers; logits, selection and weights bit-exact
-    with the oracle's fixed order"""
-    log(f"router large path R={R} E={E}")
+def _adversarial(rng, shape, f32):
+    """values across 2^-12 .. 2^12 with exact zeros of both signs and subnormals (bf16 rows when not f32)"""
+    v = (rng.standard_normal(shape) * np.exp2(rng.integers(-12, 13, shape))).astype(np.float32)
+    m = rng.random(shape)
+    v[m < 0.05] = 0.0
+    v[(m >= 0.05) & (m < 0.1)] = -0.0
+    v[(m >= 0.1) & (m < 0.13)] *= np.float32(2.0 ** -130)               # fp32 / bf16 subnormals
+    if f32:
+        return v
+    return (v.view(np.uint32) >> 16).astype(np.uint16)                    # truncation to bf16 bits
+
+
+@pytest.mark.parametrize("R,E,adv", [(300, 160, False), (4100, 200, False), (40, 64, True)])
+def test_router_large_path_partial_tiles(dev, R, E, adv):
+    """the large path's segment GEMM (fp32 MFMA, 128 rows x 64 experts per workgroup) on partial tiles: 300 and 4100
+    rows with fewer experts than a whole tile covers, and 40 rows of adversarial operands (magnitudes across 2^+-12,
+    signed zeros, subnormals); the folded logits, the selection and the weights bit-exact with the oracle's fixed
+    order (each MFMA is a fmaf chain over its 4 k)"""
+    log(f"router large path R={R} E={E} adversarial={adv}")
     rng = np.random.default_rng(R + E)
-    x = x_rows(7 + R, R)
-    wg = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    if adv:
+        x, wg = _adversarial(rng, (R, H), False), _adversarial(rng, (E, H), True)
+    else:
+        x = x_rows(7 + R, R)
+        wg = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
     bias = (rng.standard_normal(E) * 0.001).astype(np.float32)
     lg_ref = O.router_logits(x, wg)
     sel_ref, rw_ref = O.router_select(lg_ref, bias)
@@ -105,6 +121,12 @@ def test_router_large_path_partial_tiles(dev, R, E):
     sel = torch.empty((R, 8), dtype=torch.int64, device=dev); rw = torch.empty((R, 8), dtype=torch.float16, device=dev)
     router.router_fused(xt, torch.from_numpy(wg).to(dev), torch.from_numpy(bias).to(dev), logits, ctr, sel, rw, 8, 2.5)
     torch.cuda.synchronize()
+    # the large path leaves the 8 segment planes [8][R][256] in logits: folded in order from +0 they are the logits
+    seg = logits[:8 * R * 256].view(8, R, 256).cpu().numpy()[:, :, :E]
+    tot = np.zeros((R, E), np.float32)
+    for s_ in range(8):
+        tot = (tot + seg[s_]).astype(np.float32)
+    assert np.array_equal(tot.view(np.uint32), np.asarray(lg_ref, np.float32).view(np.uint32))
     assert np.array_equal(sel.cpu().numpy(), sel_ref)
     assert np.array_equal(u16(rw), rw_ref)
 
