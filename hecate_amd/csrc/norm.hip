@@ -53,7 +53,12 @@ __global__ void __launch_bounds__(1024) cn_kernel(CnArgs p)
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
     f32x4 x[2] = {z, z};
     int np = 0;
-    if (MODE == CN_PARTS) np = *p.nparts;
+    if (MODE == CN_PARTS) np = min(max(*p.nparts, 0), MAX_PARTS);
+    // the norm weights of both column halves, in flight while the residual is formed (a thread with one half reads its
+    // first twice)
+    f32x4 w4[2];
+    #pragma unroll
+    for (int k = 0; k < 2; ++k) w4[k] = load_w4<WDT>(p.w, hb ? t + 1024 * k : t);
     // with the CPU tier: its partial is o2, once the job the norm + router posted has finished (cn.cu:114-119 waits for
     // CPU_DONE the same way); when the wait runs out, or no job of this step was posted, nothing is added for it
     const float* o2 = p.o2;
@@ -64,48 +69,71 @@ __global__ void __launch_bounds__(1024) cn_kernel(CnArgs p)
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
         o2 = cpu_ok ? p.cmb->out : nullptr;
     }
-    #pragma unroll
-    for (int k = 0; k < 2; ++k)
+    if constexpr (MODE == CN_PARTS)
     {
-        if (k && !hb) break;
-        const size_t i = ro + 4 * (size_t) (t + 1024 * k);
-        const f32x4 rr = *(const f32x4*) (p.r + i);
-        f32x4 a;
-        if (MODE == CN_COMBINE)
+        // the parts of both column halves are loaded in one batch of up to 8 once the part count is in (a part past
+        // the count moves no bytes: one CU per row reads all of them), then added in part order from 0 (dec_d_kernel's
+        // sum); counts past 8 take further batches
+        constexpr size_t PS = (size_t) MAXR * H;
+        const size_t ih[2] = {ro + 4 * (size_t) t, ro + 4 * (size_t) (t + 1024)};
+        f32x4 rr[2] = {z, z}, a[2] = {z, z};
+        for (int q0 = 0; q0 < np || q0 == 0; q0 += 8)
         {
-            a = p.f ? *(const f32x4*) (p.f + i) : z;
-            a += *(const f32x4*) (p.y + i);
-            if (p.o) a += *(const f32x4*) (p.o + i);
-            if (o2) a += *(const f32x4*) (o2 + i);
-            *(f32x4*) (p.y + i) = z;
-            x[k] = a + rr;
-        }
-        else if (MODE == CN_ADD || MODE == CN_ROUTE)
-        {
-            if (p.y)
+            f32x4 pv[2][8];
+            #pragma unroll
+            for (int k = 0; k < 2; ++k)
             {
-                x[k] = *(const f32x4*) (p.y + i) + rr;
-                if (MODE == CN_ADD) *(f32x4*) (p.y + i) = z;
-            }
-            else x[k] = rr;
-        }
-        else
-        {
-            // the parts in batches of 8 loads (a part past the count is read from inside the buffer and not added),
-            // added in part order from 0 (dec_d_kernel's sum)
-            a = z;
-            for (int q0 = 0; q0 < np; q0 += 8)
-            {
-                f32x4 pv[8];
+                if (k && !hb) break;
+                if (q0 == 0) rr[k] = *(const f32x4*) (p.r + ih[k]);
                 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    pv[j] = *(const f32x4*) (p.y32 + (size_t) min(q0 + j, MAX_PARTS - 1) * MAXR * H + i);
-                #pragma unroll
-                for (int j = 0; j < 8; ++j) a = q0 + j < np ? a + pv[j] : a;
+                    pv[k][j] = q0 + j < np ? *(const f32x4*) (p.y32 + (q0 + j) * PS + ih[k]) : z;
             }
-            x[k] = a + rr;
+            #pragma unroll
+            for (int k = 0; k < 2; ++k)
+            {
+                if (k && !hb) break;
+                #pragma unroll
+                for (int j = 0; j < 8; ++j) a[k] = q0 + j < np ? a[k] + pv[k][j] : a[k];
+            }
         }
-        *(f32x4*) (p.r + i) = x[k];
+        #pragma unroll
+        for (int k = 0; k < 2; ++k)
+        {
+            if (k && !hb) break;
+            x[k] = a[k] + rr[k];
+            *(f32x4*) (p.r + ih[k]) = x[k];
+        }
+    }
+    else
+    {
+        #pragma unroll
+        for (int k = 0; k < 2; ++k)
+        {
+            if (k && !hb) break;
+            const size_t i = ro + 4 * (size_t) (t + 1024 * k);
+            const f32x4 rr = *(const f32x4*) (p.r + i);
+            f32x4 a;
+            if (MODE == CN_COMBINE)
+            {
+                a = p.f ? *(const f32x4*) (p.f + i) : z;
+                a += *(const f32x4*) (p.y + i);
+                if (p.o) a += *(const f32x4*) (p.o + i);
+                if (o2) a += *(const f32x4*) (o2 + i);
+                *(f32x4*) (p.y + i) = z;
+                x[k] = a + rr;
+            }
+            else
+            {
+                if (p.y)
+                {
+                    x[k] = *(const f32x4*) (p.y + i) + rr;
+                    if (MODE == CN_ADD) *(f32x4*) (p.y + i) = z;
+                }
+                else x[k] = rr;
+            }
+            *(f32x4*) (p.r + i) = x[k];
+        }
     }
     float s = chain4(0.f, x[0]);
     if (hb) s = chain4(s, x[1]);
@@ -118,14 +146,14 @@ __global__ void __launch_bounds__(1024) cn_kernel(CnArgs p)
     {
         if (k && !hb) break;
         const int c = t + 1024 * k;
-        f32x4 w4 = load_w4<WDT>(p.w, c);
-        if (p.cbias != 0.f) w4 += p.cbias;
+        f32x4 wk = w4[k];
+        if (p.cbias != 0.f) wk += p.cbias;
         u32x2 o;
         f16x4 oh;
         #pragma unroll
         for (int e = 0; e < 4; ++e)
         {
-            const float v = (x[k][e] * w4[e]) * rmf;
+            const float v = (x[k][e] * wk[e]) * rmf;
             const uint16_t b = XDT == WT_BF16 ? hmoe_f2bf(v) : hmoe_f2h(v);
             if (e & 1) o[e >> 1] |= (uint32_t) b << 16; else o[e >> 1] = b;
             oh[e] = XDT == WT_BF16 ? (_Float16) bf2f(b) : __builtin_bit_cast(_Float16, b);
