@@ -9,7 +9,8 @@
 // 16 WN TN tokens; wave (wm, wn) holds TM weight tiles (TM / NMAT of each matrix) x TN token tiles of 16 x 16 in its
 // accumulators. K runs in stages of 64:
 // both operands of a stage go to LDS by direct global-to-LDS loads, in a ring of 3 stages issued two ahead, so the
-// one wait and barrier per stage find the stage long arrived. A stage holds each 8 rows' 128 bytes as a 1 KB block:
+// one wait and barrier per stage find the stage long arrived; each 32-k step's fragments are read one step ahead of
+// its MFMAs. A stage holds each 8 rows' 128 bytes as a 1 KB block:
 // one load per block, lane l taking row l / 8's 16-byte chunk (l % 8) ^ (l / 8) (whole 128-byte lines from memory),
 // stored at 16 l; the swizzle puts the 16 rows x 16 bytes of an MFMA fragment read (row l % 16, chunk 4 ks + l / 16)
 // on distinct banks. Each 32-k step reads the wave's TM + TN fragments and runs TM TN MFMAs. A token past N reads
@@ -92,41 +93,48 @@ dgemm_kernel(
     for (int i = 0; i < TM; ++i)
         #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = (f32x4) {0.f, 0.f, 0.f, 0.f};
-    #pragma unroll
-    for (int s = 0; s < NST - 1; ++s) stage(s);
-    for (int s = 0; s < KS; ++s)
-    {
-        // stage s is complete when at most the NST - 2 later stages' loads are outstanding
+    // the wave's fragments of one 32-k step of a stage
+    f16x8 a[2][TM], bv[2][TN];
+    auto read = [&](const u32x4* cur, int ks) {
+        #pragma unroll
+        for (int i = 0; i < TM; ++i)
+        {
+            const int tile = (i / TMO) * WM * TMO + wm * TMO + i % TMO;
+            a[ks][i] = as_f16x8(cur[tile * 128 + fo[ks]]);
+        }
+        #pragma unroll
+        for (int j = 0; j < TN; ++j) bv[ks][j] = as_f16x8(cur[(AT + wn * TN + j) * 128 + fo[ks]]);
+    };
+    // stage s is complete when at most the NST - 2 stages issued after it are outstanding
+    auto arrive = [&]() {
         asm volatile("s_waitcnt vmcnt(%0)" :: "n"((NST - 2) * SL) : "memory");
         __syncthreads();
-        const u32x4* cur = lds[s % NST];
-        // both 32-k steps' fragments are read first (in issue order, so the first step's MFMAs wait only for their
-        // own reads), then the first step's MFMAs, the next stage's loads (issued while those MFMAs run) and the second
-        // step's MFMAs: one LDS latency per stage
-        f16x8 a[2][TM], bv[2][TN];
-        #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-        {
-            #pragma unroll
-            for (int i = 0; i < TM; ++i)
-            {
-                const int tile = (i / TMO) * WM * TMO + wm * TMO + i % TMO;
-                a[ks][i] = as_f16x8(cur[tile * 128 + fo[ks]]);
-            }
-            #pragma unroll
-            for (int j = 0; j < TN; ++j) bv[ks][j] = as_f16x8(cur[(AT + wn * TN + j) * 128 + fo[ks]]);
-        }
+    };
+    #pragma unroll
+    for (int s = 0; s < NST - 1; ++s) stage(s);
+    arrive();
+    read(lds[0], 0);
+    // each step's fragments are read one step ahead of its MFMAs, so no wave waits out an LDS latency: a stage's
+    // second step is read before its first step's MFMAs, the next stage's first step (after its wait and barrier)
+    // before this stage's second step's MFMAs; the next stage's loads go out between the two steps
+    for (int s = 0; s < KS; ++s)
+    {
+        read(lds[s % NST], 1);
         #pragma unroll
         for (int i = 0; i < TM; ++i)
             #pragma unroll
             for (int j = 0; j < TN; ++j) acc[i][j] = mfma16(a[0][i], bv[0][j], acc[i][j]);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2 * (TM + TN), 0);   // the LDS reads
-        __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);         // then the first step's MFMAs
+        __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);       // the second step's LDS reads
+        __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);       // then the first step's MFMAs
         stage(s + NST - 1);
+        arrive();                                                      // stage s + 1 (past the last: the stand-in)
+        read(lds[(s + 1) % NST], 0);
         #pragma unroll
         for (int i = 0; i < TM; ++i)
             #pragma unroll
             for (int j = 0; j < TN; ++j) acc[i][j] = mfma16(a[1][i], bv[1][j], acc[i][j]);
+        __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);       // the next stage's first-step reads
+        __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);       // then the second step's MFMAs
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     // lane l holds output rows 4 (l / 16) .. + 4 of each weight tile for token 16 j + l % 16 of its token tiles
