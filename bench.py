@@ -202,7 +202,7 @@ def partial_workload(torch, synth, steps, warmup, dev, n_layers=4):
     return out
 
 
-def tiered_workload(torch, synth, steps, warmup, dev, threads=8):
+def tiered_workload(torch, synth, steps, warmup, dev, threads=16):
     """config 3 with the other 80 experts on the host-CPU tier (tier_split.py's split): route on the GPU, hand the
     rows to the pool through the device-mapped mailbox, run the 176 resident experts into the fp32 partial
     meanwhile, then add the pool's partial on the same stream; one layer, 32 seeded inputs per row count"""
