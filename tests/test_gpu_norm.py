@@ -115,3 +115,32 @@ def test_norm_route_bit_exact(dev, R, gdt, xdt, wdt, cbias, cscale):
 
 def bits_t(t):
     return t.view(torch.int32) if t.dtype == torch.float32 else t.view(torch.int16)
+
+
+@pytest.mark.parametrize("R,nparts", [(4, 0), (4, 1), (4, 5), (4, 8), (4, 9), (16, 16), (16, 17), (2, 33)])
+def test_decode_combine_norm_part_counts(dev, R, nparts):
+    """the decode stack's output launch fused with the next norm (hmoe_decode_combine_norm): the down launch's part
+    partials summed in part order from +0 (as many as its count says, across the batch boundaries of 8), r = s + r, xn
+    = RMSNorm(r) in the rms_norm_kernel order: r and xn bit-exact against the oracle; parts past the count are never
+    added (they hold values that would change the bits)"""
+    from hecate_amd._lib import DT_BF16, DT_F32, call, ptr, stream_of
+    log(f"decode_combine_norm R={R} parts={nparts}")
+    MAX_PARTS, MAXR = 33, 16
+    g = torch.Generator().manual_seed(100 * R + nparts)
+    y32 = torch.randn((MAX_PARTS, MAXR, H), generator=g)
+    r = torch.randn((R, H), generator=g) * 3.0
+    w = (1.0 + 0.02 * torch.randn(H, generator=g)).float()
+    s = np.zeros((R, H), np.float32)
+    yh = y32.numpy()
+    for p in range(nparts):
+        s = f32(s + yh[p, :R])
+    r_ref = f32(s + r.numpy())
+    xn_ref = O.rmsnorm_cn(r_ref, f32(w.numpy()), 1e-5, 0.0, 1.0, bf16=True)
+    y32d, rd, wd = y32.to(dev), r.to(dev), w.to(dev)
+    ctr = torch.tensor([nparts, 0, 0, 0], dtype=torch.int32, device=dev)
+    xn = torch.empty((R, H), dtype=torch.bfloat16, device=dev)
+    call("hmoe_decode_combine_norm", ptr(y32d), ptr(ctr), R, ptr(rd), ptr(wd), ptr(xn), None, 1e-5, 0.0, 1.0, DT_F32,
+         DT_BF16, stream_of(dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(rd), r_ref.view(np.int32))
+    assert np.array_equal(bits(xn), xn_ref)
