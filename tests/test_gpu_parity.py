@@ -691,6 +691,46 @@ def test_long_prefill_moe4t(dev, T, ordered):
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("T", [2048, 4096])
+def test_prefill_zipf_skew(dev, T):
+    """prefill under the Zipf-calibrated selection bias of the decode configs (config 1's skew): the hot experts take
+    hundreds of picks, so they run as many row blocks (128 picks on moe4p, 256 on moe4t) next to experts with a
+    handful; routing bit-exact, the bf16 output the rounding of the fp32 sum, every row within tolerance"""
+    log(f"prefill T={T} under the Zipf bias")
+    bias = synth.zipf_bias()
+    lay = gpu_layer("c2z", dev, layer=0, bias=bias, max_rows=2048)
+    hl = HostLayer(0, bias=bias)
+    x = synth.gen_x(7000 + T, T, dev)
+    xn = u16(x)
+    out = lay.prefill(x).clone()
+    torch.cuda.synchronize()
+    pf = lay._pf
+    sel_ref, rw_ref = hl.route(xn)
+    assert np.array_equal(pf.sel[:T].cpu().numpy(), sel_ref) and np.array_equal(u16(pf.rw[:T]), rw_ref)
+    counts = np.bincount(sel_ref.ravel(), minlength=E)
+    rbt = pf.rbt[:int(pf.meta[1].item())].cpu().numpy()
+    log(f"  picks per expert {counts.min()}..{counts.max()}, {len(rbt)} row blocks")
+    assert counts.max() > 2 * pf.bm                       # the skew puts several row blocks on one expert
+    y = pf.y[:T]
+    y.zero_()
+    lay.prefill_experts(pf.xh[:T], y)
+    yh = y.cpu().numpy()
+    y.zero_()
+    torch.cuda.synchronize()
+    if T <= 2048:
+        assert np.array_equal(u16(out), O.f32_to_bf16(yh))
+    else:
+        # (moe4t adds the shared expert into the partial first: the same fp32 sum, see test_long_prefill_moe4t)
+        y2 = torch.from_numpy(yh).to(dev)
+        o2 = torch.empty_like(out)
+        moe4.finish_bf16(y2, T, o2)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), o2.view(torch.int16))
+    check_all_rows(lay, hl, x, xn, yh, sel_ref, rw_ref, seed=T + 1)
+    lay._pf = None
+    torch.cuda.empty_cache()
+
+
 def test_moe4t_gemm_entry(dev):
     """moe4t.gemm (moe4t.cu:476-488): one grouped GEMM over given pick inputs, gate/up shape (both sums) and down
     shape, against torch fp32 GEMMs on the dequantised weights of each block's expert"""
